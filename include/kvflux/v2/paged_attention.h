@@ -1,0 +1,42 @@
+#pragma once
+// Causal GQA attention straight from the paged cache.
+// Same signatures and contracts as the reference's
+// include/kvflux/v2/paged_attention.h:20-33 (src/v2/paged_attention.cu:193-313).
+
+#include "kvflux/v2/paged_kv_storage.h"
+
+#include <cstddef>
+#include <vector>
+
+namespace kvflux::v2 {
+
+// Arithmetic contract of an attention call.
+//   Exact: FP32 Q and FP32 accumulation of every product; matches the
+//          double-precision CPU reference to ~1e-6 for any KV dtype.
+//   Auto:  Exact, except that 16-bit KV caches with head_size 64 or 128 and
+//          query_tokens >= 16 use the MFMA prefill kernel, where Q and the
+//          softmax weights are rounded to the cache dtype (2e-2 contract).
+//   Fast:  MFMA prefill whenever the shape allows it (16-bit KV,
+//          head_size 64/128), otherwise Exact.
+enum class AttentionPrecision { Exact, Auto, Fast };
+
+// Single request: Q/O are device FP32 [query_tokens][query_heads][head_size];
+// query i sees cache positions <= num_tokens - query_tokens + i.
+// Uses AttentionPrecision::Auto.
+void paged_attention(const PagedKVStorage& storage, const SequenceState& sequence,
+                     const float* query_device, float* output_device,
+                     std::size_t query_tokens, std::size_t query_heads);
+
+void paged_attention(const PagedKVStorage& storage, const SequenceState& sequence,
+                     const float* query_device, float* output_device,
+                     std::size_t query_tokens, std::size_t query_heads,
+                     AttentionPrecision precision);
+
+// Batch decode: one trailing query per request, Q/O device FP32
+// [num_sequences][query_heads][head_size]. Always Exact.
+void paged_attention_batch(const PagedKVStorage& storage,
+                           const std::vector<const SequenceState*>& sequences,
+                           const float* query_device, float* output_device,
+                           std::size_t query_heads);
+
+} // namespace kvflux::v2

@@ -1,0 +1,179 @@
+/*
+ * kvflux_hip.h - C ABI of the MI355X (gfx950) paged-KV data path.
+ *
+ * Everything that touches the GPU goes through these functions: the C++17
+ * control plane (kvflux::v2, same API as the reference) calls them, and so
+ * can any other host language through its FFI. No C++ or HIP types cross
+ * the boundary: plain pointers, sizes, int status codes. Streams are passed
+ * as `void*` holding a hipStream_t (NULL = the default stream).
+ *
+ * Device pointers are expected to be on the current device (see
+ * kvflux_set_device). Every hot-path entry point only enqueues work on
+ * `stream` and returns; it does not synchronise.
+ *
+ * Cache layout (reference include/kvflux/v2/paged_kv_layout.h:10-11):
+ *   key_cache  [num_blocks][num_kv_heads][block_size][head_size]
+ *   value_cache: same shape; element type `dtype`.
+ * Page ids and slot numbers are 64-bit (reference PhysicalBlockID = size_t,
+ * PhysicalSlot = uint64_t). Device kernels skip (never dereference) page ids
+ * >= num_blocks and slots >= num_blocks * block_size.
+ */
+#ifndef KVFLUX_HIP_H
+#define KVFLUX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; the C++ layer maps each onto the exception type the
+ * reference throws (reference src/v2/paged_kv_write.cu:15-19 and callers). */
+enum kvflux_status {
+    KVFLUX_OK = 0,
+    KVFLUX_ERR_INVALID_ARGUMENT = 1, /* std::invalid_argument */
+    KVFLUX_ERR_OUT_OF_RANGE = 2,     /* std::out_of_range */
+    KVFLUX_ERR_OVERFLOW = 3,         /* std::overflow_error */
+    KVFLUX_ERR_RUNTIME = 4,          /* std::runtime_error (HIP runtime failure) */
+    KVFLUX_ERR_UNSUPPORTED = 5       /* shape or dtype a kernel does not handle */
+};
+
+/* Same values as kvflux::DType (reference include/kvflux/kv_layout.h:7). */
+enum kvflux_dtype { KVFLUX_DTYPE_F16 = 0, KVFLUX_DTYPE_BF16 = 1, KVFLUX_DTYPE_F32 = 2 };
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* kvflux_last_error(void);
+int kvflux_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Runtime plumbing. These replace the CUDA runtime calls the reference makes
+ * directly: cudaMalloc of the arena (reference src/gpu_memory_pool.cpp:38-50),
+ * the DeviceGuard (src/v2/paged_kv_write.cu:28-37), cudaPointerGetAttributes
+ * (src/v2/paged_kv_write.cu:52-60), metadata uploads (paged_kv_write.cu:122-124)
+ * and cudaStreamSynchronize (paged_kv_write.cu:138).
+ * ------------------------------------------------------------------------- */
+int kvflux_device_count(int* count);
+int kvflux_get_device(int* device);
+int kvflux_set_device(int device);
+int kvflux_device_malloc(void** ptr, size_t bytes);   /* on the current device */
+int kvflux_device_free(void* ptr);
+int kvflux_host_malloc_pinned(void** ptr, size_t bytes);
+int kvflux_host_free_pinned(void* ptr);
+/* *device = owning device id if `ptr` is device memory, else -1 (never fails
+ * for host pointers; clears any sticky runtime error it provokes). */
+int kvflux_pointer_device(const void* ptr, int* device);
+/* Asynchronous copy in any direction (unified addressing). */
+int kvflux_memcpy_async(void* dst, const void* src, size_t bytes, void* stream);
+/* Synchronous copy in any direction (pageable host memory allowed). */
+int kvflux_memcpy(void* dst, const void* src, size_t bytes);
+/* Byte fill with a kernel (no memset node, safe under graph capture). */
+int kvflux_fill_bytes(void* dst, int value, size_t bytes, void* stream);
+int kvflux_stream_create(void** stream);
+int kvflux_stream_destroy(void* stream);
+int kvflux_stream_synchronize(void* stream);
+int kvflux_device_synchronize(void);
+int kvflux_event_create(void** event);
+int kvflux_event_destroy(void* event);
+int kvflux_event_record(void* event, void* stream);
+int kvflux_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---------------------------------------------------------------------------
+ * Hot path 1: paged KV write (scatter by slot).
+ * Replaces paged_kv_write_kernel + launch_write
+ * (reference src/v2/paged_kv_write.cu:62-97), called from write_paged_kv
+ * (paged_kv_write.cu:101-139).
+ *   key_new/value_new: [num_tokens][num_kv_heads][head_size] of `dtype`.
+ *   slots: device uint64 [num_tokens]; slot = page * block_size + offset.
+ * Raw bit copy. Duplicate slots are the caller's responsibility (the C++
+ * layer rejects them, as the reference does).
+ * ------------------------------------------------------------------------- */
+int kvflux_write_paged_kv(void* key_cache, void* value_cache, uint64_t num_blocks,
+                          uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size,
+                          int dtype, const void* key_new, const void* value_new,
+                          const uint64_t* slots, uint64_t num_tokens, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Hot path 2: paged KV gather (BlockTable-driven read).
+ * Replaces paged_kv_read_kernel + launch_read
+ * (reference src/v2/paged_kv_read.cu:67-102), called from read_paged_kv
+ * (paged_kv_read.cu:106-155), generalised to many sequences per launch.
+ *   block_table: device uint64 [num_seqs][max_blocks_per_seq] (the reference's
+ *                BatchBlockTable layout, include/kvflux/v2/batch_block_table.h:14-22)
+ *   seq_lens:    device uint64 [num_seqs]
+ *   out_offsets: device uint64 [num_seqs], first output token of each sequence
+ *   max_seq_len: upper bound of seq_lens (sizes the grid)
+ *   key_out/value_out: [sum of lengths][num_kv_heads][head_size] of `dtype`.
+ * Only the valid tokens of a tail page are read or written.
+ * ------------------------------------------------------------------------- */
+int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
+                           uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
+                           uint64_t head_size, int dtype, const uint64_t* block_table,
+                           uint64_t max_blocks_per_seq, const uint64_t* seq_lens,
+                           const uint64_t* out_offsets, uint64_t num_seqs,
+                           uint64_t max_seq_len, void* key_out, void* value_out,
+                           void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Hot path 3a: paged attention, split-K (flash-decoding) kernel, FP32 math.
+ * Replaces paged_attention_batch_kernel (reference src/v2/paged_attention.cu:130-153,
+ * 173-189) and, for query_tokens small, paged_attention_kernel (:108-128, 155-171).
+ * Rows: query/output device float [num_rows][query_heads][head_size].
+ *   seq_lens != NULL: row r attends to tokens [0, seq_lens[r]) of table row r
+ *                     (batch decode; kv_len = max over seq_lens).
+ *   seq_lens == NULL: every row uses table row 0 and row r attends to tokens
+ *                     [0, kv_len - num_rows + r] (causal trailing queries of one
+ *                     sequence, reference paged_attention.cu:123).
+ * scale = 1/sqrt(head_size). query_heads % num_kv_heads == 0.
+ * workspace: device scratch of at least kvflux_paged_attention_workspace_size().
+ * Deterministic: the split partials are combined in a fixed order.
+ * ------------------------------------------------------------------------- */
+int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t kv_len,
+                                          uint64_t num_kv_heads, uint64_t query_heads,
+                                          uint64_t block_size, uint64_t head_size,
+                                          size_t* bytes);
+int kvflux_paged_attention(const void* key_cache, const void* value_cache,
+                           uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
+                           uint64_t head_size, int dtype, const uint64_t* block_table,
+                           uint64_t max_blocks_per_seq, const uint64_t* seq_lens,
+                           uint64_t kv_len, uint64_t num_rows, uint64_t query_heads,
+                           const float* query, float* output, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Hot path 3b: causal paged prefill on MFMA (BF16/FP16 caches only).
+ * Replaces paged_attention_kernel for a whole-prompt call
+ * (reference src/v2/paged_attention.cu:108-128, 193-246, query_tokens = Tq).
+ * One sequence: block_table device uint64 [ceil(kv_len / block_size)],
+ * query i attends to tokens [0, kv_len - query_tokens + i].
+ * Q is rounded to the cache dtype and the softmax weights to the cache dtype
+ * before the MFMA products; accumulation and softmax are FP32.
+ * KVFLUX_ERR_UNSUPPORTED unless dtype is F16/BF16, head_size is 64 or 128
+ * and block_size divides 64.
+ * ------------------------------------------------------------------------- */
+int kvflux_paged_prefill(const void* key_cache, const void* value_cache,
+                         uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
+                         uint64_t head_size, int dtype, const uint64_t* block_table,
+                         uint64_t num_table_blocks, uint64_t kv_len, uint64_t query_tokens,
+                         uint64_t query_heads, const float* query, float* output,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Test and benchmark support (not part of the reference API).
+ * kvflux_fill_random writes `count` elements of `dtype` from a counter-based
+ * generator: element i depends only on (seed, i), so a CPU checker can
+ * recompute any element. distribution 0: uniform [-1, 1) on a 2^-23 grid;
+ * 1: approximately N(0,1) as the sum of twelve 16-bit uniforms (Irwin-Hall).
+ * 16-bit dtypes are rounded to nearest-even from the FP32 value.
+ * kvflux_compare_bytes synchronously counts differing bytes of two device
+ * buffers.
+ * ------------------------------------------------------------------------- */
+int kvflux_fill_random(void* dst, uint64_t count, int dtype, int distribution,
+                       uint64_t seed, void* stream);
+int kvflux_compare_bytes(const void* a, const void* b, uint64_t bytes, uint64_t* mismatches);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* KVFLUX_HIP_H */

@@ -1,0 +1,72 @@
+// Shared helpers of the gfx950 kernels and the C ABI implementation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "kvflux_hip.h"
+
+namespace kvflux_hip {
+
+// Records `message` as this thread's last error and returns `status`.
+int fail(int status, const char* format, ...);
+// KVFLUX_OK, or KVFLUX_ERR_RUNTIME carrying "<op>: <hip error string>".
+int hip_status(hipError_t error, const char* operation);
+// Checks the launch just enqueued (kernel configuration errors).
+int launch_status(const char* kernel);
+
+inline std::size_t dtype_bytes(int dtype) {
+    switch (dtype) {
+    case KVFLUX_DTYPE_F16:
+    case KVFLUX_DTYPE_BF16: return 2;
+    case KVFLUX_DTYPE_F32: return 4;
+    default: return 0;
+    }
+}
+
+inline hipStream_t as_stream(void* stream) { return static_cast<hipStream_t>(stream); }
+
+inline bool is_pow2(std::uint64_t x) { return x != 0 && (x & (x - 1)) == 0; }
+
+// Division of a 32-bit numerator by a runtime-invariant divisor with one
+// multiply-high, an add and a shift (round-up magic number method,
+// Granlund & Montgomery 1994): with l = ceil(log2 d) and
+// m = floor(2^32 * (2^l - d) / d) + 1, n / d = (umulhi(n, m) + n) >> l for
+// every n < 2^32 (the sum is formed in 64 bits).
+struct FastDiv {
+    std::uint32_t divisor = 1, magic = 1, shift = 0;
+
+    FastDiv() = default;
+    explicit FastDiv(std::uint32_t d) : divisor(d) {
+        std::uint32_t l = 0;
+        while ((std::uint64_t{1} << l) < d) ++l;
+        shift = l;
+        magic = static_cast<std::uint32_t>(
+                    ((std::uint64_t{1} << 32) * ((std::uint64_t{1} << l) - d)) / d) + 1;
+    }
+    __host__ __device__ std::uint32_t div(std::uint32_t n) const {
+        const std::uint64_t hi = (static_cast<std::uint64_t>(n) * magic) >> 32;
+        return static_cast<std::uint32_t>((hi + n) >> shift);
+    }
+    __host__ __device__ std::uint32_t mod(std::uint32_t n) const { return n - div(n) * divisor; }
+};
+
+// 16-byte, 8-byte, 4-byte and 2-byte raw vectors for bit-exact copies.
+struct alignas(16) V16 { std::uint32_t w[4]; };
+struct alignas(8) V8 { std::uint32_t w[2]; };
+
+// Widest power-of-two byte width (<= 16) that divides `row_bytes` and every
+// address in `ptrs`.
+inline unsigned copy_width(std::uint64_t row_bytes, const void* const* ptrs, int n) {
+    for (unsigned w = 16; w > 1; w >>= 1) {
+        if (row_bytes % w) continue;
+        bool ok = true;
+        for (int i = 0; i < n; ++i) ok &= (reinterpret_cast<std::uintptr_t>(ptrs[i]) % w) == 0;
+        if (ok) return w;
+    }
+    return 1;
+}
+
+} // namespace kvflux_hip

@@ -1,0 +1,155 @@
+// Paged KV write: scatter of K_new/V_new rows into the cache by slot.
+// Same result as the reference's paged_kv_write_kernel
+// (src/v2/paged_kv_write.cu:62-83): for token n, head h, element d,
+//   cache[((slot_n / bs * H + h) * bs + slot_n % bs) * D + d] = new[(n * H + h) * D + d]
+// for K and V. The copy is a raw bit copy, so only the element width matters.
+//
+// gfx950 mapping: a (token, head) row of D*esize bytes is moved as
+// `row_bytes / W` vectors of W bytes (W = 16 when the row and the four base
+// pointers allow it, i.e. global_load/store_dwordx4). Consecutive lanes take
+// consecutive vectors of one row, so a wavefront reads 1 KiB of contiguous
+// input and writes whole 256-byte rows (D=128, BF16). Each thread moves
+// UNROLL vectors of K and of V with all loads issued before the stores.
+#include "common.h"
+
+namespace kvflux_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+template <typename Vec>
+__global__ __launch_bounds__(kThreads) void paged_kv_write_kernel(
+    Vec* __restrict__ key_cache, Vec* __restrict__ value_cache, const Vec* __restrict__ key_new,
+    const Vec* __restrict__ value_new, const std::uint64_t* __restrict__ slots,
+    std::uint32_t total_vectors, FastDiv vectors_per_row, FastDiv heads, FastDiv block_size,
+    std::uint32_t slot_count) {
+    const std::uint32_t first = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+    Vec k[kUnroll], v[kUnroll];
+    std::uint64_t dst[kUnroll];
+    bool live[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const std::uint32_t i = first + u * kThreads;
+        live[u] = i < total_vectors;
+        dst[u] = 0;
+        if (live[u]) {
+            const std::uint32_t row = vectors_per_row.div(i);
+            const std::uint32_t col = i - row * vectors_per_row.divisor;
+            const std::uint32_t token = heads.div(row);
+            const std::uint32_t head = row - token * heads.divisor;
+            const std::uint64_t slot = slots[token];
+            live[u] = slot < slot_count;  // never write outside the arena
+            const std::uint32_t s = static_cast<std::uint32_t>(slot);
+            const std::uint32_t page = block_size.div(s);
+            const std::uint32_t offset = s - page * block_size.divisor;
+            dst[u] = ((static_cast<std::uint64_t>(page) * heads.divisor + head) *
+                          block_size.divisor + offset) * vectors_per_row.divisor + col;
+            k[u] = key_new[i];
+            v[u] = value_new[i];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        if (live[u]) {
+            key_cache[dst[u]] = k[u];
+            value_cache[dst[u]] = v[u];
+        }
+    }
+}
+
+// Same mapping with 64-bit index arithmetic, for arenas or batches whose
+// vector or slot counts do not fit in 32 bits.
+template <typename Vec>
+__global__ __launch_bounds__(kThreads) void paged_kv_write_kernel_wide(
+    Vec* __restrict__ key_cache, Vec* __restrict__ value_cache, const Vec* __restrict__ key_new,
+    const Vec* __restrict__ value_new, const std::uint64_t* __restrict__ slots,
+    std::uint64_t total_vectors, std::uint64_t vectors_per_row, std::uint64_t heads,
+    std::uint64_t block_size, std::uint64_t slot_count) {
+    const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+    for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+         i < total_vectors; i += stride) {
+        const std::uint64_t row = i / vectors_per_row, col = i % vectors_per_row;
+        const std::uint64_t token = row / heads, head = row % heads;
+        const std::uint64_t slot = slots[token];
+        if (slot >= slot_count) continue;
+        const std::uint64_t d =
+            ((slot / block_size * heads + head) * block_size + slot % block_size) *
+                vectors_per_row + col;
+        key_cache[d] = key_new[i];
+        value_cache[d] = value_new[i];
+    }
+}
+
+template <typename Vec>
+int launch(void* kc, void* vc, const void* kn, const void* vn, const std::uint64_t* slots,
+           std::uint64_t tokens, std::uint64_t heads, std::uint64_t block_size,
+           std::uint64_t row_bytes, std::uint64_t slot_count, hipStream_t stream) {
+    const std::uint64_t vpr = row_bytes / sizeof(Vec);
+    const std::uint64_t total = tokens * heads * vpr;
+    // 32-bit path: the last thread index (grid * per_block) must not wrap.
+    constexpr std::uint64_t limit = 0xffffffffULL - kThreads * kUnroll;
+    if (total <= limit && slot_count <= limit && vpr <= limit && heads <= limit &&
+        block_size <= limit) {
+        const std::uint64_t per_block = kThreads * kUnroll;
+        const auto grid = static_cast<unsigned>((total + per_block - 1) / per_block);
+        hipLaunchKernelGGL(paged_kv_write_kernel<Vec>, dim3(grid), dim3(kThreads), 0, stream,
+                           static_cast<Vec*>(kc), static_cast<Vec*>(vc),
+                           static_cast<const Vec*>(kn), static_cast<const Vec*>(vn), slots,
+                           static_cast<std::uint32_t>(total),
+                           FastDiv(static_cast<std::uint32_t>(vpr)),
+                           FastDiv(static_cast<std::uint32_t>(heads)),
+                           FastDiv(static_cast<std::uint32_t>(block_size)),
+                           static_cast<std::uint32_t>(slot_count));
+    } else {
+        const std::uint64_t blocks = (total + kThreads - 1) / kThreads;
+        const auto grid = static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+        hipLaunchKernelGGL(paged_kv_write_kernel_wide<Vec>, dim3(grid), dim3(kThreads), 0, stream,
+                           static_cast<Vec*>(kc), static_cast<Vec*>(vc),
+                           static_cast<const Vec*>(kn), static_cast<const Vec*>(vn), slots, total,
+                           vpr, heads, block_size, slot_count);
+    }
+    return launch_status("paged_kv_write_kernel");
+}
+
+} // namespace
+} // namespace kvflux_hip
+
+using namespace kvflux_hip;
+
+extern "C" int kvflux_write_paged_kv(void* key_cache, void* value_cache, uint64_t num_blocks,
+                                     uint64_t num_kv_heads, uint64_t block_size,
+                                     uint64_t head_size, int dtype, const void* key_new,
+                                     const void* value_new, const uint64_t* slots,
+                                     uint64_t num_tokens, void* stream) {
+    if (num_tokens == 0) return KVFLUX_OK;
+    const std::size_t esize = dtype_bytes(dtype);
+    if (esize == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+    if (!key_cache || !value_cache || !key_new || !value_new || !slots) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged KV write: null pointer");
+    }
+    if (num_blocks == 0 || num_kv_heads == 0 || block_size == 0 || head_size == 0) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged KV write: zero dimension");
+    }
+    if (head_size > (~0ULL) / esize || num_blocks > (~0ULL) / block_size) {
+        return fail(KVFLUX_ERR_OVERFLOW, "paged KV write: size overflow");
+    }
+    const std::uint64_t row_bytes = head_size * esize;
+    const std::uint64_t slot_count = num_blocks * block_size;
+    const void* ptrs[4] = {key_cache, value_cache, key_new, value_new};
+    const unsigned width = copy_width(row_bytes, ptrs, 4);
+    const hipStream_t s = as_stream(stream);
+    switch (width) {
+    case 16: return launch<V16>(key_cache, value_cache, key_new, value_new, slots, num_tokens,
+                                num_kv_heads, block_size, row_bytes, slot_count, s);
+    case 8: return launch<V8>(key_cache, value_cache, key_new, value_new, slots, num_tokens,
+                              num_kv_heads, block_size, row_bytes, slot_count, s);
+    case 4: return launch<std::uint32_t>(key_cache, value_cache, key_new, value_new, slots,
+                                         num_tokens, num_kv_heads, block_size, row_bytes,
+                                         slot_count, s);
+    case 2: return launch<std::uint16_t>(key_cache, value_cache, key_new, value_new, slots,
+                                         num_tokens, num_kv_heads, block_size, row_bytes,
+                                         slot_count, s);
+    default: return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged KV write: misaligned buffers");
+    }
+}
