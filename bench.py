@@ -1,0 +1,387 @@
+"""Benchmark of the paged-KV data path on one MI355X.
+
+Prints ONE JSON line (stdout). Progress goes to stderr.
+
+Headline (`value`): batch GQA decode PagedAttention, B=128 rows with
+seq_len ~ U[1024, 32768], 32 query / 8 KV heads, head_size 128,
+block_size 16, BF16 K/V ~ N(0,1), FP32 Q ~ N(0,1), a 2048-token prefix
+shared by every row through the same physical pages, the other pages drawn
+from a seeded permutation of a 2^18-page pool. `value` is HBM throughput in
+TB/s over the UNIQUE bytes the step must read (shared prefix pages once) plus
+Q, O and the tables; logical bytes are reported next to it.
+
+Also measured in the same run (sub-objects of the JSON line):
+  write  : slot-mapped KV write, 4096 tokens x 8 heads x 128, BF16, 65536-page pool
+  gather : BlockTable gather, 64 sequences with L ~ U[512, 8192], H=8, D=128,
+           FP16 and BF16, odd pages of a full 65536-page pool
+  cpu_baseline : the CPU oracle (gather + double-precision attention, one
+           thread) on a bounded sample of the decode rows, timed here.
+
+Every timed region launches through the C ABI on a dedicated stream with all
+inputs and metadata already resident in HBM; HIP events on that stream give
+the average kernel time per launch.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "decode paged-attn HBM TB/s (% of peak) + KV write/gather GB/s, 1 GPU"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def fragment_pool(pool, order: np.ndarray) -> None:
+    """Allocates every page, then frees `order` reversed so that subsequent
+    allocations return the pages in `order` (LIFO free list)."""
+    holders = [pool.allocate() for _ in range(pool.capacity())]
+    for idx in order[::-1]:
+        pool.free(holders[int(idx)])
+    keep = np.ones(pool.capacity(), bool)
+    keep[order] = False
+    return [holders[i] for i in np.nonzero(keep)[0]]
+
+
+def time_launches(launch, stream, warmup: int, steps: int) -> float:
+    """Average milliseconds per launch measured with HIP events on `stream`."""
+    from kvflux_amd import device
+    for _ in range(warmup):
+        launch()
+    device.synchronize(stream)
+    start, stop = device.Event(), device.Event()
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    stop.record(stream)
+    return start.elapsed_ms(stop) / steps
+
+
+# --------------------------------------------------------------------- decode
+def bench_decode(v2, args, stream):
+    from kvflux_amd import capi, device
+    from oracle import oracle
+
+    B, H, Hq, D, bs, prefix = 128, 8, 32, 128, 16, 2048
+    rng = np.random.default_rng(args.seed)
+    lens = rng.integers(1024, 32768 + 1, B)
+    pool = v2.PhysicalBlockPool(1 << 18, bs)
+    storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
+    fragment_pool(pool, rng.permutation(pool.capacity()))
+    cache = v2.PrefixCache(pool)
+    base = v2.SequenceState(10**9, pool)
+    base.append_tokens(prefix)
+    tokens = list(range(prefix))
+    for blk in range(prefix // bs):
+        cache.publish_computed_block(base, blk, tokens[: (blk + 1) * bs])
+    seqs = []
+    for i, L in enumerate(lens.tolist()):
+        s = v2.SequenceState(i, pool)
+        shared = cache.attach_cached_prefix(s, tokens[: min(L, prefix)])
+        s.append_tokens(L - shared)
+        seqs.append(s)
+    table = v2.build_batch_block_table(seqs)
+    flat = np.array(table.block_table(), np.uint64)
+    width = table.max_blocks_per_sequence()
+    n_elems = storage.layout().cache_bytes() // 2
+    device.fill_random(storage.key_base(), n_elems, capi.DTYPE_BF16, 1, args.seed + 1)
+    device.fill_random(storage.value_base(), n_elems, capi.DTYPE_BF16, 1, args.seed + 2)
+    q = device.DeviceBuffer(B * Hq * D * 4)
+    o = device.DeviceBuffer(B * Hq * D * 4)
+    device.fill_random(q.ptr, B * Hq * D, capi.DTYPE_F32, 1, args.seed + 3)
+    td = device.to_device(flat)
+    ld = device.to_device(lens.astype(np.uint64))
+    ws = C.c_size_t(0)
+    capi.call("kvflux_paged_attention_workspace_size", B, int(lens.max()), H, Hq, bs, D, C.byref(ws))
+    wd = device.DeviceBuffer(ws.value)
+    wd.fill(0)
+    device.synchronize()
+    lib = capi.lib()
+    kb, vb, max_len = storage.key_base(), storage.value_base(), int(lens.max())
+
+    def launch():
+        capi.check(lib.kvflux_paged_attention(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16,
+                                              td.ptr, width, ld.ptr, max_len, B, Hq, q.ptr, o.ptr,
+                                              wd.ptr, ws.value, stream))
+
+    ms = time_launches(launch, stream, args.warmup, args.steps)
+    out = o.download(np.float32)
+
+    # Bytes: every (page, kv head) row read once, counted by unique page.
+    mat = flat.reshape(B, width)
+    tok_per_page = {}
+    for r in range(B):
+        L = int(lens[r])
+        for blk in range((L + bs - 1) // bs):
+            page = int(mat[r, blk])
+            tok_per_page[page] = max(tok_per_page.get(page, 0), min(bs, L - blk * bs))
+    kv_token_bytes = H * D * 2 * 2  # K and V, BF16, all kv heads
+    io_bytes = 2 * B * Hq * D * 4 + flat.nbytes + lens.size * 8
+    unique_bytes = sum(tok_per_page.values()) * kv_token_bytes + io_bytes
+    logical_bytes = int(lens.sum()) * kv_token_bytes + io_bytes
+    flops = 4 * Hq * D * int(lens.sum())
+
+    # CPU oracle on a bounded sample of rows (copied to a compact host cache).
+    sample_rows = list(range(args.cpu_rows))
+    qh = q.download(np.float32).reshape(B, Hq * D)
+    page_bytes = H * bs * D * 2
+    err = 0.0
+    cpu_s = 0.0
+    cpu_bytes = 0
+    for r in sample_rows:
+        L = int(lens[r])
+        npg = (L + bs - 1) // bs
+        pages = mat[r, :npg]
+        kc = np.empty(npg * page_bytes // 2, np.uint16)
+        vc = np.empty_like(kc)
+        for j, pg in enumerate(pages.tolist()):
+            kc[j * page_bytes // 2:(j + 1) * page_bytes // 2] = device.memcpy_d2h(kb + pg * page_bytes, page_bytes, np.uint16)
+            vc[j * page_bytes // 2:(j + 1) * page_bytes // 2] = device.memcpy_d2h(vb + pg * page_bytes, page_bytes, np.uint16)
+        local = np.arange(npg, dtype=np.uint64)
+        t0 = time.perf_counter()
+        ref = oracle.paged_attention_rows(kc, vc, H, bs, D, oracle.BF16, local, npg,
+                                          np.array([L], np.uint64), qh[r], Hq, threads=1)
+        cpu_s += time.perf_counter() - t0
+        cpu_bytes += L * kv_token_bytes
+        err = max(err, float(np.abs(ref - out[r * Hq * D:(r + 1) * Hq * D]).max()))
+    del seqs, base
+    return {
+        "ms": ms,
+        "unique_bytes": unique_bytes,
+        "logical_bytes": logical_bytes,
+        "flops": flops,
+        "sum_len": int(lens.sum()),
+        "max_abs_err": err,
+        "cpu": {"value": cpu_bytes / cpu_s / 1e12, "unit": "TB/s", "cores": 1, "kind": "port",
+                "seconds": cpu_s,
+                "sample": f"{len(sample_rows)} decode rows (L={[int(lens[r]) for r in sample_rows]}, "
+                          "32 q heads each): page gather + double-precision softmax attention, 1 thread"},
+    }
+
+
+# --------------------------------------------------------------------- write
+def bench_write(v2, args, stream):
+    from kvflux_amd import capi, device
+    from oracle import oracle
+
+    N_SEQ, NEW, H, D, bs = 256, 16, 8, 128, 16
+    rng = np.random.default_rng(args.seed + 10)
+    pool = v2.PhysicalBlockPool(65536, bs)
+    storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
+    fragment_pool(pool, rng.permutation(pool.capacity()))
+    prefix_lens = rng.integers(0, 2048, N_SEQ)
+    seqs = []
+    writes = []
+    for i, L0 in enumerate(prefix_lens.tolist()):
+        s = v2.SequenceState(i, pool)
+        s.append_tokens(L0 + NEW)
+        seqs.append(s)
+        writes += [(s, L0 + j) for j in range(NEW)]
+    slots = np.array(v2.build_slot_mapping(writes), np.uint64)
+    N = slots.size
+    n = N * H * D
+    kn, vn = device.DeviceBuffer(n * 2), device.DeviceBuffer(n * 2)
+    device.fill_random(kn.ptr, n, capi.DTYPE_BF16, 1, args.seed + 11)
+    device.fill_random(vn.ptr, n, capi.DTYPE_BF16, 1, args.seed + 12)
+    lib = capi.lib()
+    capi.call("kvflux_fill_bytes", C.c_void_p(storage.key_base()), 0xA5, storage.layout().total_bytes(), None)
+    sd = device.to_device(slots)
+    device.synchronize()
+    kb, vb = storage.key_base(), storage.value_base()
+
+    def launch():
+        capi.check(lib.kvflux_write_paged_kv(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16,
+                                             kn.ptr, vn.ptr, sd.ptr, N, stream))
+
+    ms = time_launches(launch, stream, args.warmup, max(args.steps, 50))
+    # Full synchronous C++ API call (host validation + upload + kernel + sync).
+    slot_list = slots.tolist()
+    for _ in range(3):
+        v2.write_paged_kv(storage, kn.ptr, vn.ptr, slot_list)
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        v2.write_paged_kv(storage, kn.ptr, vn.ptr, slot_list)
+    api_us = (time.perf_counter() - t0) / reps * 1e6
+
+    # Bit-exact check of every touched page (and its untouched slots).
+    page_elems = H * bs * D
+    pages = np.unique(slots // bs)
+    remap = {int(p): j for j, p in enumerate(pages.tolist())}
+    host_k = np.full(pages.size * page_elems, 0xA5A5, np.uint16)
+    host_v = host_k.copy()
+    oracle.write_paged_kv(host_k, host_v, H, bs, D, oracle.BF16, kn.download(np.uint16),
+                          vn.download(np.uint16),
+                          np.array([remap[int(s // bs)] * bs + int(s % bs) for s in slots], np.uint64))
+    mism = 0
+    for j, pg in enumerate(pages.tolist()):
+        gk = device.memcpy_d2h(kb + pg * page_elems * 2, page_elems * 2, np.uint16)
+        gv = device.memcpy_d2h(vb + pg * page_elems * 2, page_elems * 2, np.uint16)
+        mism += int((gk != host_k[j * page_elems:(j + 1) * page_elems]).sum())
+        mism += int((gv != host_v[j * page_elems:(j + 1) * page_elems]).sum())
+    del seqs
+    bytes_step = 2 * 2 * N * H * D * 2 + N * 8
+    return {"kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9, "bytes": bytes_step,
+            "api_us": api_us, "tokens": N, "pages_checked": int(pages.size), "mismatched_elements": mism}
+
+
+# --------------------------------------------------------------------- gather
+def bench_gather(v2, args, stream, dtype_name: str):
+    from kvflux_amd import capi, device
+    from oracle import oracle
+
+    S, H, D, bs = 64, 8, 128, 16
+    code = capi.DTYPE_F16 if dtype_name == "Float16" else capi.DTYPE_BF16
+    rng = np.random.default_rng(args.seed + 20)
+    lens = rng.integers(512, 8192 + 1, S)
+    pool = v2.PhysicalBlockPool(65536, bs)
+    storage = v2.PagedKVStorage(pool, H, D, getattr(v2.DType, dtype_name))
+    odd = np.arange(1, pool.capacity(), 2)
+    fragment_pool(pool, rng.permutation(odd))
+    seqs = []
+    for i, L in enumerate(lens.tolist()):
+        s = v2.SequenceState(i, pool)
+        s.append_tokens(L)
+        seqs.append(s)
+    t = v2.build_batch_block_table(seqs)
+    flat = np.array(t.block_table(), np.uint64)
+    width = t.max_blocks_per_sequence()
+    assert all(int(p) % 2 == 1 for p in flat if p < 2**63)
+    n_elems = storage.layout().cache_bytes() // 2
+    device.fill_random(storage.key_base(), n_elems, code, 1, args.seed + 21)
+    device.fill_random(storage.value_base(), n_elems, code, 1, args.seed + 22)
+    total = int(lens.sum())
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    out_bytes = total * H * D * 2
+    ko, vo = device.DeviceBuffer(out_bytes), device.DeviceBuffer(out_bytes)
+    td, ld, od = device.to_device(flat), device.to_device(lens.astype(np.uint64)), device.to_device(offs)
+    device.synchronize()
+    lib = capi.lib()
+    kb, vb = storage.key_base(), storage.value_base()
+    max_len = int(lens.max())
+
+    def launch():
+        capi.check(lib.kvflux_gather_paged_kv(kb, vb, pool.capacity(), H, bs, D, code, td.ptr, width,
+                                              ld.ptr, od.ptr, S, max_len, ko.ptr, vo.ptr, stream))
+
+    ms = time_launches(launch, stream, args.warmup, args.steps)
+    # Bit-exact check of a few sequences against the oracle gather.
+    page_elems = H * bs * D
+    mism = 0
+    mat = flat.reshape(S, width)
+    for r in (0, S // 2, S - 1):
+        L = int(lens[r])
+        npg = (L + bs - 1) // bs
+        kc = np.concatenate([device.memcpy_d2h(kb + int(p) * page_elems * 2, page_elems * 2, np.uint16)
+                             for p in mat[r, :npg]])
+        vc = np.concatenate([device.memcpy_d2h(vb + int(p) * page_elems * 2, page_elems * 2, np.uint16)
+                             for p in mat[r, :npg]])
+        ek, ev = oracle.gather_paged_kv(kc, vc, H, bs, D, code, np.arange(npg, dtype=np.uint64), L)
+        gk = device.memcpy_d2h(ko.ptr + int(offs[r]) * H * D * 2, L * H * D * 2, np.uint16)
+        gv = device.memcpy_d2h(vo.ptr + int(offs[r]) * H * D * 2, L * H * D * 2, np.uint16)
+        mism += int((gk != ek).sum() + (gv != ev).sum())
+    pages = int(sum((int(L) + bs - 1) // bs for L in lens))
+    bytes_step = 8192 * total + 8 * pages
+    del seqs
+    return {"dtype": dtype_name, "kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9,
+            "bytes": bytes_step, "tokens": total, "mismatched_elements_sampled": mism}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--cpu-rows", type=int, default=2)
+    ap.add_argument("--skip-aux", action="store_true", help="decode only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}); run with --gpus 1.", file=sys.stderr)
+        return 2
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs as a single process on one GPU", file=sys.stderr)
+        return 2
+
+    import kvflux_amd
+    from kvflux_amd import capi, device
+
+    v2 = kvflux_amd.v2
+    if capi.device_count() < 1:
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    capi.call("kvflux_set_device", 0)
+    stream = device.Stream()
+
+    log("decode ...")
+    dec = bench_decode(v2, args, stream.handle)
+    log(f"decode {dec['ms']:.3f} ms, err {dec['max_abs_err']:.2e}")
+    aux = {}
+    if not args.skip_aux:
+        log("write ...")
+        aux["write"] = bench_write(v2, args, stream.handle)
+        log(f"write {aux['write']}")
+        for name in ("BFloat16", "Float16"):
+            log(f"gather {name} ...")
+            aux[f"gather_{name}"] = bench_gather(v2, args, stream.handle, name)
+            log(f"gather {aux[f'gather_{name}']}")
+
+    s = dec["ms"] * 1e-3
+    achieved = dec["unique_bytes"] / s / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(dec["unique_bytes"] / s / 1e12, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 KV, fp32 math",
+        "data": "synthetic (counter-based N(0,1) generator, seeded)",
+        "config": {
+            "workload": "batch GQA decode PagedAttention: B=128, seq_len U[1024,32768], 32 q / 8 kv heads, "
+                        "head_size 128, block_size 16, BF16 KV, FP32 Q/O, 2048-token shared prefix, "
+                        "2^18-page pool",
+            "seed": args.seed,
+            "sum_seq_len": dec["sum_len"],
+        },
+        "pct_of_peak": round(100 * achieved / PEAK_HBM_GBPS, 2),
+        "logical_TBps": round(dec["logical_bytes"] / s / 1e12, 4),
+        "tokens_per_s": round(128 / s, 1),
+        "decode_max_abs_err_vs_oracle": dec["max_abs_err"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+            "kernel": "paged_attention_split_kernel<Bf16,128,4>",
+            "bytes_per_launch": dec["unique_bytes"],
+        },
+        "cpu_baseline": dec["cpu"],
+    }
+    for k, v in aux.items():
+        line[k] = v
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -125,8 +125,12 @@ int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
  *                     [0, kv_len - num_rows + r] (causal trailing queries of one
  *                     sequence, reference paged_attention.cu:123).
  * scale = 1/sqrt(head_size). query_heads % num_kv_heads == 0.
- * workspace: device scratch of at least kvflux_paged_attention_workspace_size().
- * Deterministic: the split partials are combined in a fixed order.
+ * workspace: device scratch of at least kvflux_paged_attention_workspace_size()
+ *   bytes (no initialisation needed). Calls that share a workspace must be
+ *   ordered (same stream).
+ * Rows longer than one 512-token split take two launches: the split kernel
+ * and a combine kernel that merges the split partials in ascending split
+ * order, so results are deterministic.
  * ------------------------------------------------------------------------- */
 int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t kv_len,
                                           uint64_t num_kv_heads, uint64_t query_heads,

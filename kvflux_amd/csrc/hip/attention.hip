@@ -27,6 +27,7 @@
 #include "common.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace kvflux_hip {
 namespace {
@@ -400,6 +401,370 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attention_split_kernel(Para
     }
 }
 
+// ---------------------------------------------------------------- MFMA QK decode
+// 16-bit caches, head_size 64 or 128: the QK product of each 16-token tile
+// runs on v_mfma_f32_16x16x32_{bf16,f16}. Lane l of the A operand holds
+// K[token l%16][8*(l/16) + 32*kk ...] exactly as loaded (no conversion); the
+// B operand holds Q split into three 16-bit parts (hi + mid + lo = q to
+// FP32 precision) in columns split*G + g, so one MFMA per 32 dims gives all
+// partial scores and two DPP row shifts add the parts. The softmax is online
+// per wavefront (exact running max, rescale only when it grows), P*V stays on
+// the VALU in the 8-lanes-per-token layout, and each wavefront double-buffers
+// the K and V loads of its next tile.
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+template <typename E>
+struct Mfma;
+template <>
+struct Mfma<Bf16> {
+    using Vec = bf16x8_t;
+    using Elem = __bf16;
+    __device__ static std::uint16_t split(float x, float* rest) {  // RNE to BF16
+        std::uint32_t u = __float_as_uint(x);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        const std::uint16_t h = static_cast<std::uint16_t>(u >> 16);
+        *rest = x - __uint_as_float(static_cast<std::uint32_t>(h) << 16);
+        return h;
+    }
+    __device__ static f32x4_t mma(const Vec& a, const Vec& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Mfma<F16> {
+    using Vec = f16x8_t;
+    using Elem = _Float16;
+    __device__ static std::uint16_t split(float x, float* rest) {
+        const _Float16 h = static_cast<_Float16>(x);
+        *rest = x - static_cast<float>(h);
+        return __builtin_bit_cast(std::uint16_t, h);
+    }
+    __device__ static f32x4_t mma(const Vec& a, const Vec& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <int kShift>
+__device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 16-lane row
+    if constexpr (kShift == 0) {
+        return x;
+    } else {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + kShift, 0xf, 0xf, true));
+    }
+}
+
+// ---------------------------------------------------------------- block_size 16 decode
+// Hot path for 16-token pages, 16-bit caches, head_size 64/128:
+//  * persistent workgroups walk a plan of (row, 512-token chunk, kv head)
+//    items built in LDS from the row lengths (exclusive prefix of chunk
+//    counts), so no workgroup is launched for an empty chunk and consecutive
+//    items read the same pages for neighbouring kv heads;
+//  * a 16-token tile is exactly one page: its id is one uniform LDS read and
+//    every K/V address is that page's base plus a constant lane offset;
+//  * QK^T of a tile is kD/32 MFMA 16x16x32 ops on the raw 16-bit K rows
+//    against Q split into hi/mid/lo 16-bit parts (FP32-equivalent); two DPP
+//    row shifts add the parts;
+//  * online softmax per wavefront, P*V on the VALU (8 lanes per token row),
+//    K and V of the next tile in flight while the current one is computed.
+constexpr int kPlanRows = 4096;
+
+template <typename E, int kD, int kG>
+__global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p) {
+    using M = Mfma<E>;
+    using Vec = typename M::Vec;
+    using T = typename E::Storage;
+    constexpr int kBs = 16;
+    constexpr int kSteps = kD / 32;
+    constexpr int kDpl = kD == 64 ? 8 : 16;
+    constexpr int kLpt = kD / kDpl;
+    constexpr int kTpp = 64 / kLpt;
+    constexpr int kPasses = kBs / kTpp;
+    constexpr int kVWords = kDpl / 2;
+    constexpr int kMfmas = 3 * kG <= 16 ? 1 : 2;
+    constexpr int kTiles = kChunk / kBs;
+    static_assert(kLpt == 8 && kTpp == 8 && kPasses == 2, "V lane layout");
+
+    __shared__ std::uint32_t plan[kPlanRows + 1];
+    __shared__ std::uint32_t scan[kThreads];
+    __shared__ std::uint64_t pages[kTiles];
+    __shared__ __attribute__((aligned(16))) std::uint16_t qsplit[3 * kG * kD];
+    __shared__ __attribute__((aligned(16))) float probs[kWaves][kBs * kG];
+    __shared__ float reduce[kWaves * 2 * kG * kD];
+    __shared__ float wstats[kWaves][2 * kG];
+
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const int col = lane % 16, quad = lane / 16;
+    const int tsub = lane / kLpt, slice = lane % kLpt;
+    const std::uint32_t rows = p.num_rows;
+
+    // ---- plan: plan[r] = number of chunks of rows < r (a zero-length row
+    // still owns one chunk so its output is written).
+    constexpr int kPer = kPlanRows / kThreads;
+    std::uint32_t mine = 0;
+    for (int i = 0; i < kPer; ++i) {
+        const std::uint32_t r = tid * kPer + i;
+        if (r < rows) {
+            const std::uint64_t len = row_length(p, r);
+            mine += len == 0 ? 1u : static_cast<std::uint32_t>((len + kChunk - 1) / kChunk);
+        }
+    }
+    scan[tid] = mine;
+    __syncthreads();
+    for (int off = 1; off < kThreads; off <<= 1) {
+        const std::uint32_t add = tid >= off ? scan[tid - off] : 0u;
+        __syncthreads();
+        scan[tid] += add;
+        __syncthreads();
+    }
+    {
+        std::uint32_t run = scan[tid] - mine;
+        for (int i = 0; i < kPer; ++i) {
+            const std::uint32_t r = tid * kPer + i;
+            if (r < rows) {
+                plan[r] = run;
+                const std::uint64_t len = row_length(p, r);
+                run += len == 0 ? 1u : static_cast<std::uint32_t>((len + kChunk - 1) / kChunk);
+            }
+        }
+        if (tid == kThreads - 1) plan[rows] = scan[tid];
+    }
+    __syncthreads();
+    const std::uint32_t total = plan[rows] * p.heads;
+
+    const T* kc = static_cast<const T*>(p.key_cache);
+    const T* vc = static_cast<const T*>(p.value_cache);
+    const std::uint64_t head_stride = static_cast<std::uint64_t>(kBs) * kD;
+    const std::uint64_t page_stride = head_stride * p.heads;
+    // Lane offsets inside one page-head block [16 tokens][kD].
+    const std::uint32_t k_lane = col * kD + quad * 8;
+    const std::uint32_t v_lane = tsub * kD + slice * kDpl;
+    float* my_probs = probs[wave];
+
+    for (std::uint32_t item = blockIdx.x; item < total; item += gridDim.x) {
+        const std::uint32_t kvh = item % p.heads;
+        const std::uint32_t rc = item / p.heads;
+        std::uint32_t lo = 0, hi = rows;  // plan[lo] <= rc < plan[hi]
+        while (hi - lo > 1) {
+            const std::uint32_t mid = (lo + hi) / 2;
+            if (plan[mid] <= rc) lo = mid; else hi = mid;
+        }
+        const std::uint32_t row = lo;
+        const std::uint32_t chunk = rc - plan[row];
+        const std::uint64_t len = row_length(p, row);
+        const std::uint64_t tok_begin = static_cast<std::uint64_t>(chunk) * kChunk;
+        const std::uint32_t ntok =
+            len > tok_begin ? static_cast<std::uint32_t>(len - tok_begin < kChunk ? len - tok_begin : kChunk) : 0;
+        const std::uint32_t ntiles = (ntok + kBs - 1) / kBs;
+        const std::uint64_t* table_row = p.table + (p.seq_lens ? row : 0) * p.width;
+        const std::uint64_t first_page = tok_begin / kBs;
+        for (std::uint32_t i = tid; i < ntiles; i += kThreads) {
+            const std::uint64_t logical = first_page + i;
+            const std::uint64_t id = logical < p.width ? table_row[logical] : kNoPage;
+            pages[i] = id < p.num_blocks ? id : kNoPage;
+        }
+        const std::uint32_t qh0 = kvh * kG;
+        for (int idx = tid; idx < kG * kD; idx += kThreads) {
+            const int g = idx / kD, d = idx % kD;
+            float rest;
+            const float x = p.query[(static_cast<std::uint64_t>(row) * p.query_heads + qh0 + g) * kD + d] * p.scale_log2;
+            qsplit[(0 * kG + g) * kD + d] = M::split(x, &rest);
+            qsplit[(1 * kG + g) * kD + d] = M::split(rest, &rest);
+            qsplit[(2 * kG + g) * kD + d] = M::split(rest, &rest);
+        }
+        __syncthreads();
+
+        // B operands from the split table: column -> (split, head).
+        Vec qb[kMfmas][kSteps];
+#pragma unroll
+        for (int m = 0; m < kMfmas; ++m) {
+            int split = col / kG, g = col % kG;
+            bool used = col < 3 * kG;
+            if (kMfmas == 2 && m == 1) {
+                split = 2;
+                g = col;
+                used = col < kG;
+            }
+#pragma unroll
+            for (int kk = 0; kk < kSteps; ++kk) {
+                const uint4 raw = used ? *reinterpret_cast<const uint4*>(qsplit + (split * kG + g) * kD + kk * 32 + quad * 8)
+                                       : make_uint4(0, 0, 0, 0);
+                qb[m][kk] = __builtin_bit_cast(Vec, raw);
+            }
+        }
+
+        struct Tile {
+            uint4 k[kSteps];
+            uint4 v[kPasses][kVWords / 4];
+        };
+        auto load = [&](std::uint32_t t, Tile& b) {
+            const std::uint64_t page = pages[t];
+            if (page != kNoPage) {
+                const T* kb = kc + page * page_stride + kvh * head_stride;
+                const T* vb = vc + page * page_stride + kvh * head_stride;
+#pragma unroll
+                for (int kk = 0; kk < kSteps; ++kk) b.k[kk] = *reinterpret_cast<const uint4*>(kb + k_lane + kk * 32);
+#pragma unroll
+                for (int u = 0; u < kPasses; ++u)
+#pragma unroll
+                    for (int w = 0; w < kVWords / 4; ++w)
+                        b.v[u][w] = *reinterpret_cast<const uint4*>(vb + v_lane + u * kTpp * kD + w * 8);
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < kSteps; ++kk) b.k[kk] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < kPasses; ++u)
+#pragma unroll
+                    for (int w = 0; w < kVWords / 4; ++w) b.v[u][w] = make_uint4(0, 0, 0, 0);
+            }
+        };
+
+        float run_max = -INFINITY, run_sum = 0.0f;
+        float acc[kG][kDpl];
+#pragma unroll
+        for (int g = 0; g < kG; ++g)
+#pragma unroll
+            for (int i = 0; i < kDpl; ++i) acc[g][i] = 0.0f;
+
+        auto compute = [&](std::uint32_t t, Tile& b) {
+            const std::uint32_t valid = pages[t] == kNoPage ? 0u
+                                        : (ntok - t * kBs < kBs ? ntok - t * kBs : kBs);  // uniform
+            f32x4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < kSteps; ++kk) {
+                const Vec a = __builtin_bit_cast(Vec, b.k[kk]);
+                s0 = M::mma(a, qb[0][kk], s0);
+                if constexpr (kMfmas == 2) s1 = M::mma(a, qb[1][kk], s1);
+            }
+            float sc[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (kMfmas == 1) {
+                    sc[r] = s0[r] + row_shl<kG>(s0[r]) + row_shl<2 * kG>(s0[r]);
+                } else {
+                    sc[r] = s0[r] + row_shl<kG>(s0[r]) + s1[r];
+                }
+            }
+            if (valid < kBs) {  // partial or unreadable tile (uniform)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (static_cast<std::uint32_t>(quad * 4 + r) >= valid) sc[r] = -INFINITY;
+                }
+#pragma unroll
+                for (int u = 0; u < kPasses; ++u) {
+                    if (static_cast<std::uint32_t>(u * kTpp + tsub) >= valid) {
+#pragma unroll
+                        for (int w = 0; w < kVWords / 4; ++w) b.v[u][w] = make_uint4(0, 0, 0, 0);
+                    }
+                }
+            }
+            float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            tmax = fmaxf(tmax, swizzle_xor16(tmax));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float new_max = fmaxf(run_max, tmax);
+            const float alpha = exp2_shifted(run_max, new_max);
+            run_max = new_max;
+            float psum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pr = exp2_shifted(sc[r], new_max);
+                psum += pr;
+                if (col < kG) my_probs[(quad * 4 + r) * kG + col] = pr;
+            }
+            run_sum = run_sum * alpha + psum;
+#pragma unroll
+            for (int g = 0; g < kG; ++g) {
+                const float a_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
+                if (a_g != 1.0f) {
+#pragma unroll
+                    for (int i = 0; i < kDpl; ++i) acc[g][i] *= a_g;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < kPasses; ++u) {
+                const std::uint32_t* words = reinterpret_cast<const std::uint32_t*>(b.v[u]);
+                float v[kDpl];
+                widen<E>(words, v, kDpl);
+                float pw[kG];
+#pragma unroll
+                for (int g = 0; g < kG; ++g) pw[g] = my_probs[(u * kTpp + tsub) * kG + g];
+#pragma unroll
+                for (int g = 0; g < kG; ++g)
+#pragma unroll
+                    for (int i = 0; i < kDpl; ++i) acc[g][i] = fmaf(pw[g], v[i], acc[g][i]);
+            }
+            __builtin_amdgcn_wave_barrier();
+        };
+
+        Tile buf0, buf1;
+        std::uint32_t t0 = wave;
+        if (t0 < ntiles) load(t0, buf0);
+        for (; t0 < ntiles; t0 += 2 * kWaves) {
+            const std::uint32_t t1 = t0 + kWaves;
+            if (t1 < ntiles) load(t1, buf1);
+            compute(t0, buf0);
+            if (t1 >= ntiles) break;
+            if (t1 + kWaves < ntiles) load(t1 + kWaves, buf0);
+            compute(t1, buf1);
+        }
+
+        // Wave totals, then the block combine through LDS.
+        run_sum += swizzle_xor16(run_sum);
+        run_sum += __shfl_xor(run_sum, 32);
+        if (lane < kG) {
+            wstats[wave][2 * lane] = run_max;
+            wstats[wave][2 * lane + 1] = run_sum;
+        }
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+#pragma unroll
+            for (int i = 0; i < kDpl; ++i) {
+                float a = acc[g][i];
+                a += dpp<kRowRor8>(a);
+                a += swizzle_xor16(a);
+                acc[g][i] = a;
+            }
+        }
+        if ((lane & 31) < kLpt) {
+            float* dst = reduce + ((wave * 2 + lane / 32) * kG) * kD + slice * kDpl;
+#pragma unroll
+            for (int g = 0; g < kG; ++g)
+#pragma unroll
+                for (int i = 0; i < kDpl; ++i) dst[g * kD + i] = acc[g][i];
+        }
+        __syncthreads();
+
+        const bool single = len <= kChunk || p.max_chunks <= 1;
+        for (int idx = tid; idx < kG * kD; idx += kThreads) {
+            const int g = idx / kD, d = idx % kD;
+            float m = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) m = fmaxf(m, wstats[w][2 * g]);
+            float l = 0.0f, sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float f = exp2_shifted(wstats[w][2 * g], m);
+                l += wstats[w][2 * g + 1] * f;
+                sum += (reduce[(w * 2) * kG * kD + idx] + reduce[(w * 2 + 1) * kG * kD + idx]) * f;
+            }
+            const std::uint64_t out_row = static_cast<std::uint64_t>(row) * p.query_heads + qh0 + g;
+            if (single) {
+                p.output[out_row * kD + d] = l > 0.0f ? sum / l : 0.0f;
+            } else {
+                const std::uint64_t slot = out_row * p.max_chunks + chunk;
+                p.partial_acc[slot * kD + d] = sum;
+                if (d == 0) {
+                    p.partial_ml[2 * slot] = m;
+                    p.partial_ml[2 * slot + 1] = l;
+                }
+            }
+        }
+        __syncthreads();  // LDS is reused by the next item
+    }
+}
+
 // Combines the chunk partials of every (row, query head) with more than one
 // chunk, in ascending chunk order.
 __global__ __launch_bounds__(64) void paged_attention_combine_kernel(Params p, std::uint32_t head_dim) {
@@ -545,9 +910,61 @@ int launch_generic(Params p, std::uint64_t rows, std::uint64_t head_dim, hipStre
     return KVFLUX_OK;
 }
 
+// Persistent grid: every resident workgroup slot gets one workgroup.
+template <typename E, int kD, int kG>
+int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s) {
+    static int slots = 0;  // resident workgroups per device (queried once)
+    if (slots == 0) {
+        int device = 0, cus = 0, per_cu = 0;
+        int status = hip_status(hipGetDevice(&device), "hipGetDevice");
+        if (status == KVFLUX_OK)
+            status = hip_status(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                                "hipDeviceGetAttribute");
+        if (status == KVFLUX_OK)
+            status = hip_status(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                    &per_cu, paged_decode_bs16_kernel<E, kD, kG>, kThreads, 0),
+                                "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+        if (status != KVFLUX_OK) return status;
+        slots = cus * (per_cu > 0 ? per_cu : 1);
+    }
+    const std::uint64_t items = static_cast<std::uint64_t>(p.num_rows) * max_chunks * p.heads;
+    const unsigned grid = static_cast<unsigned>(items < static_cast<std::uint64_t>(slots) ? items : slots);
+    p.row_base = 0;
+    hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG>), dim3(grid), dim3(kThreads), 0, s, p);
+    int status = launch_status("paged_decode_bs16_kernel");
+    if (status != KVFLUX_OK) return status;
+    if (max_chunks > 1) {
+        for (std::uint64_t base = 0; base < p.num_rows; base += 0x7fffffffULL / p.query_heads) {
+            const std::uint64_t n = p.num_rows - base < 0x7fffffffULL / p.query_heads
+                                        ? p.num_rows - base : 0x7fffffffULL / p.query_heads;
+            p.row_base = static_cast<std::uint32_t>(base);
+            hipLaunchKernelGGL(paged_attention_combine_kernel, dim3(static_cast<unsigned>(n * p.query_heads)),
+                               dim3(64), 0, s, p, static_cast<std::uint32_t>(kD));
+            status = launch_status("paged_attention_combine_kernel");
+            if (status != KVFLUX_OK) return status;
+        }
+    }
+    return KVFLUX_OK;
+}
+
 template <typename E, int kD>
 int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint64_t max_chunks,
                    hipStream_t s) {
+    if constexpr (!std::is_same<E, F32>::value && (kD == 64 || kD == 128)) {
+        if (p.block_size.divisor == 16 && rows <= kPlanRows) {
+            switch (group) {
+            case 1: return launch_bs16<E, kD, 1>(p, max_chunks, s);
+            case 2: return launch_bs16<E, kD, 2>(p, max_chunks, s);
+            case 4: return launch_bs16<E, kD, 4>(p, max_chunks, s);
+            case 8:
+                // D=128 with 8 heads per group needs 128 accumulators per
+                // lane: the FP32 split kernel (8 dims per lane) fits better.
+                if constexpr (kD == 64) return launch_bs16<E, kD, 8>(p, max_chunks, s);
+                break;
+            default: break;
+            }
+        }
+    }
     switch (group) {
     case 1: return launch_split<E, kD, 1>(p, rows, max_chunks, s);
     case 2: return launch_split<E, kD, 2>(p, rows, max_chunks, s);

@@ -74,8 +74,9 @@ public:
     }
     DeviceBuffer(const DeviceBuffer&) = delete;
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-    // Current device must be the owning device.
-    void* reserve(std::size_t bytes) {
+    // Current device must be the owning device. A new allocation is
+    // zero-filled when `zeroed` (the attention workspace relies on it).
+    void* reserve(std::size_t bytes, bool zeroed = false) {
         if (bytes <= bytes_) return ptr_;
         if (ptr_) check(kvflux_device_free(ptr_), "free scratch");
         ptr_ = nullptr;
@@ -83,6 +84,7 @@ public:
         const std::size_t rounded = (bytes + 4095) & ~std::size_t{4095};
         check(kvflux_device_malloc(&ptr_, rounded), "allocate scratch");
         bytes_ = rounded;
+        if (zeroed) check(kvflux_fill_bytes(ptr_, 0, rounded, nullptr), "clear scratch");
         return ptr_;
     }
     std::size_t size() const noexcept { return bytes_; }

@@ -178,6 +178,7 @@ def test_c_abi_attention_and_errors(gpu):
     capi.check(lib.kvflux_paged_attention_workspace_size(2, 1000, H, Hq, bs, D, C.byref(ws)))
     assert ws.value > 0
     wd = device.DeviceBuffer(ws.value)
+    wd.fill(0)
     capi.check(lib.kvflux_paged_attention(kc.ptr, vc.ptr, blocks, H, bs, D, capi.DTYPE_BF16, td.ptr, 63,
                                           ld.ptr, 1000, 2, Hq, qd.ptr, od.ptr, wd.ptr, ws.value, None))
     device.synchronize()
