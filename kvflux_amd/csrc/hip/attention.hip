@@ -417,10 +417,30 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 template <typename E>
 struct Mfma;
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+
 template <>
 struct Mfma<Bf16> {
     using Vec = bf16x8_t;
     using Elem = __bf16;
+    // x = hi + mid + lo exactly up to the last 8 bits: truncating splits.
+    __device__ static void split3(float x, std::uint32_t& hi, std::uint32_t& mid, std::uint32_t& lo) {
+        hi = __float_as_uint(x) & 0xffff0000u;
+        const float r1 = x - __uint_as_float(hi);
+        mid = __float_as_uint(r1) & 0xffff0000u;
+        const float r2 = r1 - __uint_as_float(mid);
+        lo = __float_as_uint(r2) & 0xffff0000u;
+    }
+    // Packs the 16-bit payloads of four split words (upper halves).
+    __device__ static i16x4_t pack(const std::uint32_t* w) {
+        const std::uint32_t a = (w[0] >> 16) | (w[1] & 0xffff0000u);
+        const std::uint32_t b = (w[2] >> 16) | (w[3] & 0xffff0000u);
+        return __builtin_bit_cast(i16x4_t, make_uint2(a, b));
+    }
+    __device__ static f32x4_t mma16(const i16x4_t& a, const i16x4_t& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
     __device__ static std::uint16_t split(float x, float* rest) {  // RNE to BF16
         std::uint32_t u = __float_as_uint(x);
         u += 0x7fffu + ((u >> 16) & 1u);
@@ -436,6 +456,25 @@ template <>
 struct Mfma<F16> {
     using Vec = f16x8_t;
     using Elem = _Float16;
+    // Three FP16 parts, each holding its value in the upper 16 bits.
+    __device__ static void split3(float x, std::uint32_t& hi, std::uint32_t& mid, std::uint32_t& lo) {
+        const _Float16 h = static_cast<_Float16>(x);
+        const float r1 = x - static_cast<float>(h);
+        const _Float16 m = static_cast<_Float16>(r1);
+        const _Float16 l = static_cast<_Float16>(r1 - static_cast<float>(m));
+        hi = static_cast<std::uint32_t>(__builtin_bit_cast(std::uint16_t, h)) << 16;
+        mid = static_cast<std::uint32_t>(__builtin_bit_cast(std::uint16_t, m)) << 16;
+        lo = static_cast<std::uint32_t>(__builtin_bit_cast(std::uint16_t, l)) << 16;
+    }
+    __device__ static i16x4_t pack(const std::uint32_t* w) {
+        const std::uint32_t a = (w[0] >> 16) | (w[1] & 0xffff0000u);
+        const std::uint32_t b = (w[2] >> 16) | (w[3] & 0xffff0000u);
+        return __builtin_bit_cast(i16x4_t, make_uint2(a, b));
+    }
+    __device__ static f32x4_t mma16(const i16x4_t& a, const i16x4_t& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                                     __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+    }
     __device__ static std::uint16_t split(float x, float* rest) {
         const _Float16 h = static_cast<_Float16>(x);
         *rest = x - static_cast<float>(h);
@@ -445,6 +484,15 @@ struct Mfma<F16> {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
 };
+
+template <int kShift>
+__device__ inline std::uint32_t row_shr_u(std::uint32_t x) {  // lane i <- lane i-kShift in a row
+    return static_cast<std::uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x110 + kShift, 0xf, 0xf, true));
+}
+template <int kShift>
+__device__ inline float row_shr(float x) {
+    return __uint_as_float(row_shr_u<kShift>(__float_as_uint(x)));
+}
 
 template <int kShift>
 __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 16-lane row
@@ -462,13 +510,61 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 //    counts), so no workgroup is launched for an empty chunk and consecutive
 //    items read the same pages for neighbouring kv heads;
 //  * a 16-token tile is exactly one page: its id is one uniform LDS read and
-//    every K/V address is that page's base plus a constant lane offset;
+//    every K/V address is that page's base plus a constant lane offset, and
+//    both K and V of a tile arrive as fully coalesced 16-byte loads;
 //  * QK^T of a tile is kD/32 MFMA 16x16x32 ops on the raw 16-bit K rows
 //    against Q split into hi/mid/lo 16-bit parts (FP32-equivalent); two DPP
 //    row shifts add the parts;
-//  * online softmax per wavefront, P*V on the VALU (8 lanes per token row),
-//    K and V of the next tile in flight while the current one is computed.
+//  * online softmax per wavefront; the weights P are split the same way and
+//    P*V runs as kD/16 MFMA 16x16x16 ops: V^T (the A operand) comes from the
+//    wave's own LDS copy of the tile through the transposing ds_read_tr16_b64,
+//    and P^T (the B operand) is exactly the four weights each score lane
+//    holds (tokens 4*quad .. 4*quad+3 of its column);
+//  * K and V of the next tile are in flight while the current one is computed.
+// V tile in LDS: row t (token) holds kD 16-bit values as kD/8 chunks of 16
+// bytes; chunk c of row t is stored at slot c ^ ((kD/64) * (t % 8)), which
+// makes both the row-wise 16-byte writes and the transposing 8-byte reads
+// free of bank conflicts.
 constexpr int kPlanRows = 4096;
+
+// Column routing of the three split parts of a per-head value held by lanes
+// col < kG of each 16-lane row: set 0 gets hi in columns [0, kG), mid in
+// [kG, 2kG) and, when 3kG <= 16, lo in [2kG, 3kG); otherwise lo goes to the
+// second set (columns [0, kG), handled by the caller). Lanes whose column is
+// not covered keep hi (those output columns are never read). With kG a
+// multiple of 4 the moves are bank-masked DPP writes of whole 4-lane banks.
+template <int kShift, int kBanks>
+__device__ inline std::uint32_t dpp_shr_into(std::uint32_t old, std::uint32_t src) {
+    return static_cast<std::uint32_t>(__builtin_amdgcn_update_dpp(
+        static_cast<int>(old), static_cast<int>(src), 0x110 + kShift, 0xf, kBanks, false));
+}
+
+// x *= a with the result tied to x's register (a plain multiply under a
+// rarely taken branch makes the register allocator copy every accumulator
+// on the other path).
+__device__ inline void scale_in_place(f32x4_t& v, float a) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float x = v[r];
+        asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(a));
+        v[r] = x;
+    }
+}
+
+template <int kG, int kSets>
+__device__ inline std::uint32_t route(std::uint32_t hi, std::uint32_t mid, std::uint32_t lo, int col) {
+    if constexpr (kG == 4) {
+        return dpp_shr_into<8, 0x4>(dpp_shr_into<4, 0x2>(hi, mid), lo);
+    } else if constexpr (kG == 8) {
+        static_assert(kSets == 2, "lo of 8 heads goes to the second set");
+        return dpp_shr_into<8, 0xc>(hi, mid);
+    } else {
+        const std::uint32_t mid_up = row_shr_u<kG>(mid), lo_up = row_shr_u<2 * kG>(lo);
+        return col < kG ? hi : col < 2 * kG ? mid_up : col < 3 * kG ? lo_up : hi;
+    }
+}
+
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
 template <typename E, int kD, int kG>
 __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p) {
@@ -476,38 +572,44 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     using Vec = typename M::Vec;
     using T = typename E::Storage;
     constexpr int kBs = 16;
-    constexpr int kSteps = kD / 32;
-    constexpr int kDpl = kD == 64 ? 8 : 16;
-    constexpr int kLpt = kD / kDpl;
-    constexpr int kTpp = 64 / kLpt;
-    constexpr int kPasses = kBs / kTpp;
-    constexpr int kVWords = kDpl / 2;
-    constexpr int kMfmas = 3 * kG <= 16 ? 1 : 2;
-    constexpr int kTiles = kChunk / kBs;
-    static_assert(kLpt == 8 && kTpp == 8 && kPasses == 2, "V lane layout");
+    constexpr int kSteps = kD / 32;         // QK MFMAs per tile (32 dims each)
+    constexpr int kDt = kD / 16;            // P*V MFMAs per tile (16 dims each)
+    constexpr int kCpr = kD / 8;            // 16-byte chunks per token row
+    constexpr int kVLoads = kD / 32;        // 16-byte V chunks per lane per tile
+    constexpr int kRowStep = 64 / kCpr;     // token rows covered by one wave-wide load
+    constexpr int kSwz = kCpr / 8;          // LDS slot swizzle multiplier
+    constexpr int kSets = 3 * kG <= 16 ? 1 : 2;
+    constexpr int kTiles = kChunk / kBs;    // tiles per item
+    constexpr int kPerWave = kTiles / kWaves;
+    constexpr int kRowBytes = kD * 2;
+    constexpr int kQPer = (kG * kD + kThreads - 1) / kThreads;
+    static_assert(kRowStep * kVLoads == kBs, "V tile covers 16 tokens");
+    static_assert(kPerWave % 2 == 0 && kPerWave <= 64, "tile pairs per wave");
 
     __shared__ std::uint32_t plan[kPlanRows + 1];
+    __shared__ std::uint32_t lens[kPlanRows];
     __shared__ std::uint32_t scan[kThreads];
-    __shared__ std::uint64_t pages[kTiles];
-    __shared__ __attribute__((aligned(16))) std::uint16_t qsplit[3 * kG * kD];
-    __shared__ __attribute__((aligned(16))) float probs[kWaves][kBs * kG];
-    __shared__ float reduce[kWaves * 2 * kG * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t qsplit[2][3 * kG * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t vtile[kWaves][kBs * kD];
+    __shared__ __attribute__((aligned(16))) float reduce[kWaves * kG * kD];
     __shared__ float wstats[kWaves][2 * kG];
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int col = lane % 16, quad = lane / 16;
-    const int tsub = lane / kLpt, slice = lane % kLpt;
     const std::uint32_t rows = p.num_rows;
 
-    // ---- plan: plan[r] = number of chunks of rows < r (a zero-length row
-    // still owns one chunk so its output is written).
+    // ---- plan: lens[r] = row length (clamped to kv_len), plan[r] = number
+    // of chunks of rows < r (a zero-length row still owns one chunk so its
+    // output is written).
     constexpr int kPer = kPlanRows / kThreads;
     std::uint32_t mine = 0;
     for (int i = 0; i < kPer; ++i) {
         const std::uint32_t r = tid * kPer + i;
         if (r < rows) {
-            const std::uint64_t len = row_length(p, r);
-            mine += len == 0 ? 1u : static_cast<std::uint32_t>((len + kChunk - 1) / kChunk);
+            const std::uint64_t full = row_length(p, r);
+            const std::uint32_t len = static_cast<std::uint32_t>(full < p.kv_len ? full : p.kv_len);
+            lens[r] = len;
+            mine += len == 0 ? 1u : (len + kChunk - 1) / kChunk;
         }
     }
     scan[tid] = mine;
@@ -524,8 +626,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             const std::uint32_t r = tid * kPer + i;
             if (r < rows) {
                 plan[r] = run;
-                const std::uint64_t len = row_length(p, r);
-                run += len == 0 ? 1u : static_cast<std::uint32_t>((len + kChunk - 1) / kChunk);
+                run += lens[r] == 0 ? 1u : (lens[r] + kChunk - 1) / kChunk;
             }
         }
         if (tid == kThreads - 1) plan[rows] = scan[tid];
@@ -537,180 +638,277 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     const T* vc = static_cast<const T*>(p.value_cache);
     const std::uint64_t head_stride = static_cast<std::uint64_t>(kBs) * kD;
     const std::uint64_t page_stride = head_stride * p.heads;
-    // Lane offsets inside one page-head block [16 tokens][kD].
+    // K: lane (quad, col) loads token col, dims 8*quad + 32*kk .. +8.
     const std::uint32_t k_lane = col * kD + quad * 8;
-    const std::uint32_t v_lane = tsub * kD + slice * kDpl;
-    float* my_probs = probs[wave];
+    // V: lane loads chunk lane + 64*i of the tile (contiguous 1 KiB per load).
+    const std::uint32_t v_lane = lane * 8;
+    char* const my_tile = reinterpret_cast<char*>(vtile[wave]);
+    std::uint32_t v_store[kVLoads];  // swizzled LDS byte offset of each loaded chunk
+#pragma unroll
+    for (int i = 0; i < kVLoads; ++i) {
+        const int t = lane / kCpr + i * kRowStep, c = lane % kCpr;
+        v_store[i] = t * kRowBytes + ((c ^ (kSwz * (t % 8))) * 16);
+    }
+    // Transposing read of the 16x16 block dt: lane (q, s) addresses token
+    // 4q + s/4, dims 16*dt + 4*(s%4) .. +4. The swizzle acts on bits 4..6 of
+    // the byte offset and dt on bits 5..7, so block dt is base ^ (dt << 5).
+    std::uint32_t v_read;
+    {
+        const int s = lane % 16, t = 4 * quad + s / 4;
+        const int c = (4 * (s % 4)) / 8;
+        v_read = t * kRowBytes + ((c ^ (kSwz * (t % 8))) * 16) + (s % 2) * 8;
+    }
 
-    for (std::uint32_t item = blockIdx.x; item < total; item += gridDim.x) {
-        const std::uint32_t kvh = item % p.heads;
+    // ---- work items: (row, 512-token chunk, kv head), item = rc * H + kvh.
+    // Every global load of the item loop is unconditional (invalid tiles read
+    // page 0 and are masked), so the compiler's wait counts stay exact and
+    // the tile stream never drains.
+    struct Item {
+        std::uint32_t row, chunk, kvh, ntok;
+    };
+    auto uniform = [](std::uint32_t x) { return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x))); };
+    auto locate = [&](std::uint32_t item) -> Item {
+        Item it;
+        it.kvh = uniform(item % p.heads);
         const std::uint32_t rc = item / p.heads;
         std::uint32_t lo = 0, hi = rows;  // plan[lo] <= rc < plan[hi]
         while (hi - lo > 1) {
             const std::uint32_t mid = (lo + hi) / 2;
             if (plan[mid] <= rc) lo = mid; else hi = mid;
         }
-        const std::uint32_t row = lo;
-        const std::uint32_t chunk = rc - plan[row];
-        const std::uint64_t len = row_length(p, row);
-        const std::uint64_t tok_begin = static_cast<std::uint64_t>(chunk) * kChunk;
-        const std::uint32_t ntok =
-            len > tok_begin ? static_cast<std::uint32_t>(len - tok_begin < kChunk ? len - tok_begin : kChunk) : 0;
-        const std::uint32_t ntiles = (ntok + kBs - 1) / kBs;
-        const std::uint64_t* table_row = p.table + (p.seq_lens ? row : 0) * p.width;
-        const std::uint64_t first_page = tok_begin / kBs;
-        for (std::uint32_t i = tid; i < ntiles; i += kThreads) {
-            const std::uint64_t logical = first_page + i;
-            const std::uint64_t id = logical < p.width ? table_row[logical] : kNoPage;
-            pages[i] = id < p.num_blocks ? id : kNoPage;
-        }
-        const std::uint32_t qh0 = kvh * kG;
-        for (int idx = tid; idx < kG * kD; idx += kThreads) {
-            const int g = idx / kD, d = idx % kD;
-            float rest;
-            const float x = p.query[(static_cast<std::uint64_t>(row) * p.query_heads + qh0 + g) * kD + d] * p.scale_log2;
-            qsplit[(0 * kG + g) * kD + d] = M::split(x, &rest);
-            qsplit[(1 * kG + g) * kD + d] = M::split(rest, &rest);
-            qsplit[(2 * kG + g) * kD + d] = M::split(rest, &rest);
-        }
-        __syncthreads();
-
-        // B operands from the split table: column -> (split, head).
-        Vec qb[kMfmas][kSteps];
+        it.row = uniform(lo);
+        it.chunk = uniform(rc - plan[it.row]);
+        const std::uint32_t len = lens[it.row];
+        const std::uint32_t begin = it.chunk * kChunk;
+        it.ntok = uniform(len > begin ? (len - begin < kChunk ? len - begin : kChunk) : 0u);
+        return it;
+    };
+    // Lane j < kPerWave of every wave: element offset of the page of tile
+    // wave + kWaves * j, or kNoPage.
+    auto fetch_pages = [&](const Item& it) -> std::uint64_t {
+        const std::uint64_t* table_row = p.table + (p.seq_lens ? it.row : 0) * p.width;
+        const std::uint64_t logical = static_cast<std::uint64_t>(it.chunk) * kTiles + wave + kWaves * (lane % kPerWave);
+        const std::uint64_t id = table_row[logical < p.width ? logical : p.width - 1];
+        return logical < p.width && id < p.num_blocks ? id * page_stride : kNoPage;
+    };
+    // Query elements tid + kThreads * i of the item's kG heads (clamped).
+    auto fetch_query = [&](const Item& it, float (&q)[kQPer]) {
+        const float* base = p.query + (static_cast<std::uint64_t>(it.row) * p.query_heads + it.kvh * kG) * kD;
 #pragma unroll
-        for (int m = 0; m < kMfmas; ++m) {
-            int split = col / kG, g = col % kG;
-            bool used = col < 3 * kG;
-            if (kMfmas == 2 && m == 1) {
-                split = 2;
-                g = col;
-                used = col < kG;
-            }
+        for (int i = 0; i < kQPer; ++i) {
+            const int idx = tid + kThreads * i;
+            q[i] = base[idx < kG * kD ? idx : kG * kD - 1];
+        }
+    };
+    auto stage_query = [&](const float (&q)[kQPer], int s) {
 #pragma unroll
-            for (int kk = 0; kk < kSteps; ++kk) {
-                const uint4 raw = used ? *reinterpret_cast<const uint4*>(qsplit + (split * kG + g) * kD + kk * 32 + quad * 8)
-                                       : make_uint4(0, 0, 0, 0);
-                qb[m][kk] = __builtin_bit_cast(Vec, raw);
+        for (int i = 0; i < kQPer; ++i) {
+            const int idx = tid + kThreads * i;
+            if (idx < kG * kD) {
+                const int g = idx / kD, d = idx % kD;
+                float rest;
+                const float x = q[i] * p.scale_log2;
+                qsplit[s][(0 * kG + g) * kD + d] = M::split(x, &rest);
+                qsplit[s][(1 * kG + g) * kD + d] = M::split(rest, &rest);
+                qsplit[s][(2 * kG + g) * kD + d] = M::split(rest, &rest);
             }
         }
+    };
+    auto page_of = [](std::uint64_t pages, int j) -> std::uint64_t {
+        const std::uint32_t lo32 = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pages), j));
+        const std::uint32_t hi32 = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pages >> 32), j));
+        return (static_cast<std::uint64_t>(hi32) << 32) | lo32;
+    };
 
-        struct Tile {
-            uint4 k[kSteps];
-            uint4 v[kPasses][kVWords / 4];
-        };
-        auto load = [&](std::uint32_t t, Tile& b) {
-            const std::uint64_t page = pages[t];
-            if (page != kNoPage) {
-                const T* kb = kc + page * page_stride + kvh * head_stride;
-                const T* vb = vc + page * page_stride + kvh * head_stride;
+    struct Tile {
+        uint4 k[kSteps];
+        uint4 v[kVLoads];
+    };
+    auto load = [&](std::uint64_t off, std::uint32_t kvh, Tile& b) {
+        const std::uint64_t base = (off == kNoPage ? 0 : off) + kvh * head_stride;
+        const T* kb = kc + base + k_lane;
+        const T* vb = vc + base + v_lane;
 #pragma unroll
-                for (int kk = 0; kk < kSteps; ++kk) b.k[kk] = *reinterpret_cast<const uint4*>(kb + k_lane + kk * 32);
+        for (int kk = 0; kk < kSteps; ++kk) b.k[kk] = *reinterpret_cast<const uint4*>(kb + kk * 32);
 #pragma unroll
-                for (int u = 0; u < kPasses; ++u)
+        for (int i = 0; i < kVLoads; ++i) b.v[i] = *reinterpret_cast<const uint4*>(vb + i * 512);
+    };
+
+    // run_max is a reference point, not always the exact maximum: it only
+    // moves when a score exceeds it by more than kLazy (log2 units), so
+    // weights stay <= 2^kLazy and rescales are rare.
+    constexpr float kLazy = 8.0f;
+    float run_max, run_sum;
+    f32x4_t acc[kSets][kDt];
+    Vec qb[kSets][kSteps];
+
+    // consume(): V of the tile into the wave's LDS slot and the QK^T MFMAs;
+    // after it the tile's registers are free for the next load.
+    struct Scores {
+        f32x4_t s0, s1;
+        std::uint32_t valid;
+    };
+    auto consume = [&](std::uint32_t valid, const Tile& b) -> Scores {
+        Scores out;
+        out.valid = valid;
 #pragma unroll
-                    for (int w = 0; w < kVWords / 4; ++w)
-                        b.v[u][w] = *reinterpret_cast<const uint4*>(vb + v_lane + u * kTpp * kD + w * 8);
+        for (int i = 0; i < kVLoads; ++i) *reinterpret_cast<uint4*>(my_tile + v_store[i]) = b.v[i];
+        if (valid < kBs) {  // rows past the end read as zero (0 * NaN would poison P*V)
+#pragma unroll
+            for (int i = 0; i < kVLoads; ++i) {
+                if (static_cast<std::uint32_t>(lane / kCpr + i * kRowStep) >= valid)
+                    *reinterpret_cast<uint4*>(my_tile + v_store[i]) = make_uint4(0, 0, 0, 0);
+            }
+        }
+        out.s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        out.s1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < kSteps; ++kk) {
+            const Vec a = __builtin_bit_cast(Vec, b.k[kk]);
+            out.s0 = M::mma(a, qb[0][kk], out.s0);
+            if constexpr (kSets == 2) out.s1 = M::mma(a, qb[1][kk], out.s1);
+        }
+        return out;
+    };
+
+    // finish(): online softmax of the tile's scores and the P*V MFMAs.
+    auto finish = [&](const Scores& in) {
+        const std::uint32_t valid = in.valid;
+        // Lane (quad, col < kG) holds the scores of tokens 4*quad+r, head col.
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if constexpr (kSets == 1) {
+                sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + row_shl<2 * kG>(in.s0[r]);
             } else {
-#pragma unroll
-                for (int kk = 0; kk < kSteps; ++kk) b.k[kk] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-                for (int u = 0; u < kPasses; ++u)
-#pragma unroll
-                    for (int w = 0; w < kVWords / 4; ++w) b.v[u][w] = make_uint4(0, 0, 0, 0);
+                sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + in.s1[r];
             }
-        };
+            if (valid < kBs && static_cast<std::uint32_t>(quad * 4 + r) >= valid) sc[r] = -INFINITY;
+        }
+        float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        tmax = fmaxf(tmax, swizzle_xor16(tmax));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const bool grow = tmax > run_max + kLazy;
+        const float old_max = run_max;
+        if (grow) run_max = tmax;
+        const float ref = run_max == -INFINITY ? 0.0f : run_max;  // exp2(-inf - ref) = 0
+        const float alpha = grow ? __builtin_amdgcn_exp2f(old_max - ref) : 1.0f;
 
-        float run_max = -INFINITY, run_sum = 0.0f;
-        float acc[kG][kDpl];
+        // Weights, split into three 16-bit parts and routed to the columns
+        // (split, head): lane col < kG keeps hi, the mid and lo parts move kG
+        // and 2*kG lanes up the row.
+        std::uint32_t w0[4], w1[4];
+        float psum = 0.0f;
 #pragma unroll
-        for (int g = 0; g < kG; ++g)
-#pragma unroll
-            for (int i = 0; i < kDpl; ++i) acc[g][i] = 0.0f;
+        for (int r = 0; r < 4; ++r) {
+            const float pr = __builtin_amdgcn_exp2f(sc[r] - ref);
+            psum += pr;
+            std::uint32_t whi, wmid, wlo;
+            M::split3(pr, whi, wmid, wlo);
+            w0[r] = route<kG, kSets>(whi, wmid, wlo, col);
+            if constexpr (kSets == 2) w1[r] = wlo;
+        }
+        run_sum = run_sum * alpha + psum;
 
-        auto compute = [&](std::uint32_t t, Tile& b) {
-            const std::uint32_t valid = pages[t] == kNoPage ? 0u
-                                        : (ntok - t * kBs < kBs ? ntok - t * kBs : kBs);  // uniform
-            f32x4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        // Rescale the columns whose reference point moved (never needed while
+        // nothing has been accumulated yet).
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(col < kG && grow && old_max != -INFINITY) != 0, 0)) {
+            const float a0 = __uint_as_float(route<kG, kSets>(__float_as_uint(alpha), __float_as_uint(alpha),
+                                                              __float_as_uint(alpha), col));
 #pragma unroll
-            for (int kk = 0; kk < kSteps; ++kk) {
-                const Vec a = __builtin_bit_cast(Vec, b.k[kk]);
-                s0 = M::mma(a, qb[0][kk], s0);
-                if constexpr (kMfmas == 2) s1 = M::mma(a, qb[1][kk], s1);
+            for (int dt = 0; dt < kDt; ++dt) acc[0][dt] *= a0;
+            if constexpr (kSets == 2) {
+#pragma unroll
+                for (int dt = 0; dt < kDt; ++dt) acc[1][dt] *= alpha;
             }
-            float sc[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if constexpr (kMfmas == 1) {
-                    sc[r] = s0[r] + row_shl<kG>(s0[r]) + row_shl<2 * kG>(s0[r]);
-                } else {
-                    sc[r] = s0[r] + row_shl<kG>(s0[r]) + s1[r];
-                }
-            }
-            if (valid < kBs) {  // partial or unreadable tile (uniform)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (static_cast<std::uint32_t>(quad * 4 + r) >= valid) sc[r] = -INFINITY;
-                }
-#pragma unroll
-                for (int u = 0; u < kPasses; ++u) {
-                    if (static_cast<std::uint32_t>(u * kTpp + tsub) >= valid) {
-#pragma unroll
-                        for (int w = 0; w < kVWords / 4; ++w) b.v[u][w] = make_uint4(0, 0, 0, 0);
-                    }
-                }
-            }
-            float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-            tmax = fmaxf(tmax, swizzle_xor16(tmax));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float new_max = fmaxf(run_max, tmax);
-            const float alpha = exp2_shifted(run_max, new_max);
-            run_max = new_max;
-            float psum = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float pr = exp2_shifted(sc[r], new_max);
-                psum += pr;
-                if (col < kG) my_probs[(quad * 4 + r) * kG + col] = pr;
-            }
-            run_sum = run_sum * alpha + psum;
-#pragma unroll
-            for (int g = 0; g < kG; ++g) {
-                const float a_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
-                if (a_g != 1.0f) {
-#pragma unroll
-                    for (int i = 0; i < kDpl; ++i) acc[g][i] *= a_g;
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int u = 0; u < kPasses; ++u) {
-                const std::uint32_t* words = reinterpret_cast<const std::uint32_t*>(b.v[u]);
-                float v[kDpl];
-                widen<E>(words, v, kDpl);
-                float pw[kG];
-#pragma unroll
-                for (int g = 0; g < kG; ++g) pw[g] = my_probs[(u * kTpp + tsub) * kG + g];
-#pragma unroll
-                for (int g = 0; g < kG; ++g)
-#pragma unroll
-                    for (int i = 0; i < kDpl; ++i) acc[g][i] = fmaf(pw[g], v[i], acc[g][i]);
-            }
-            __builtin_amdgcn_wave_barrier();
-        };
-
-        Tile buf0, buf1;
-        std::uint32_t t0 = wave;
-        if (t0 < ntiles) load(t0, buf0);
-        for (; t0 < ntiles; t0 += 2 * kWaves) {
-            const std::uint32_t t1 = t0 + kWaves;
-            if (t1 < ntiles) load(t1, buf1);
-            compute(t0, buf0);
-            if (t1 >= ntiles) break;
-            if (t1 + kWaves < ntiles) load(t1 + kWaves, buf0);
-            compute(t1, buf1);
         }
 
-        // Wave totals, then the block combine through LDS.
+        const i16x4_t pb0 = M::pack(w0);
+        i16x4_t pb1;
+        if constexpr (kSets == 2) pb1 = M::pack(w1);
+#pragma unroll
+        for (int dt = 0; dt < kDt; ++dt) {
+            lds_i16x4_t* src = (lds_i16x4_t*)((__attribute__((address_space(3))) char*)(
+                                       (__attribute__((address_space(3))) std::uint16_t*)vtile[wave]) +
+                                   (v_read ^ (dt << 5)));
+            const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(src);
+            acc[0][dt] = M::mma16(va, pb0, acc[0][dt]);
+            if constexpr (kSets == 2) acc[1][dt] = M::mma16(va, pb1, acc[1][dt]);
+        }
+    };
+
+    // ---- item loop. Wave w takes tiles w, w + 4, ... (kPerWave of them) of
+    // every item; its loads run two tiles ahead through item boundaries. The
+    // next item's page offsets and query are fetched at the start of the
+    // current one.
+    std::uint32_t item = blockIdx.x;
+    if (item >= total) return;  // uniform over the block
+    int sel = 0;
+    Item cur = locate(item);
+    std::uint64_t cur_pages = fetch_pages(cur);
+    {
+        float q[kQPer];
+        fetch_query(cur, q);
+        stage_query(q, 0);
+    }
+    __syncthreads();
+    Tile buf0, buf1;
+    load(page_of(cur_pages, 0), cur.kvh, buf0);
+    load(page_of(cur_pages, 1), cur.kvh, buf1);
+    while (true) {
+        const std::uint32_t next_item = item + gridDim.x;
+        const bool has_next = next_item < total;
+        const Item nxt = locate(has_next ? next_item : item);
+        const std::uint64_t nxt_pages = fetch_pages(nxt);
+        float nq[kQPer];
+        fetch_query(nxt, nq);
+
+        // B operands from the split table: column -> (split, head). Columns
+        // past the last split only feed output columns that are never read.
+#pragma unroll
+        for (int m = 0; m < kSets; ++m) {
+            int split = col / kG, g = col % kG;
+            if (kSets == 2 && m == 1) split = 2;
+            if (split > 2) split = 2;
+#pragma unroll
+            for (int kk = 0; kk < kSteps; ++kk) {
+                qb[m][kk] = __builtin_bit_cast(
+                    Vec, *reinterpret_cast<const uint4*>(&qsplit[sel][(split * kG + g) * kD + kk * 32 + quad * 8]));
+            }
+        }
+        run_max = -INFINITY;
+        run_sum = 0.0f;
+#pragma unroll
+        for (int m = 0; m < kSets; ++m)
+#pragma unroll
+            for (int dt = 0; dt < kDt; ++dt) acc[m][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+        auto valid_of = [&](int j) -> std::uint32_t {
+            const std::uint32_t t = wave + kWaves * j;
+            const std::uint32_t begin = t * kBs;
+            const std::uint32_t n = cur.ntok > begin ? (cur.ntok - begin < kBs ? cur.ntok - begin : kBs) : 0u;
+            return page_of(cur_pages, j) == kNoPage ? 0u : n;
+        };
+        auto issue = [&](int j, Tile& b) {  // stream position j: this item's tile j or the next item's j - kPerWave
+            if (j < kPerWave) {
+                load(page_of(cur_pages, j), cur.kvh, b);
+            } else {
+                load(page_of(nxt_pages, j - kPerWave), nxt.kvh, b);
+            }
+        };
+#pragma unroll
+        for (int j = 0; j < kPerWave; j += 2) {
+            const Scores s0 = consume(valid_of(j), buf0);
+            issue(j + 2, buf0);
+            finish(s0);
+            const Scores s1 = consume(valid_of(j + 1), buf1);
+            issue(j + 3, buf1);
+            finish(s1);
+        }
+        if (has_next) stage_query(nq, sel ^ 1);
+
+        // Wave totals: add the split columns (lane col < kG then holds head
+        // col, dims 16*dt + 4*quad + r), then the block combine through LDS.
         run_sum += swizzle_xor16(run_sum);
         run_sum += __shfl_xor(run_sum, 32);
         if (lane < kG) {
@@ -718,25 +916,24 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             wstats[wave][2 * lane + 1] = run_sum;
         }
 #pragma unroll
-        for (int g = 0; g < kG; ++g) {
+        for (int dt = 0; dt < kDt; ++dt) {
+            float4 o;
+            float* op = reinterpret_cast<float*>(&o);
 #pragma unroll
-            for (int i = 0; i < kDpl; ++i) {
-                float a = acc[g][i];
-                a += dpp<kRowRor8>(a);
-                a += swizzle_xor16(a);
-                acc[g][i] = a;
+            for (int r = 0; r < 4; ++r) {
+                const float x = acc[0][dt][r];
+                if constexpr (kSets == 1) {
+                    op[r] = x + row_shl<kG>(x) + row_shl<2 * kG>(x);
+                } else {
+                    op[r] = x + row_shl<kG>(x) + acc[1][dt][r];
+                }
             }
-        }
-        if ((lane & 31) < kLpt) {
-            float* dst = reduce + ((wave * 2 + lane / 32) * kG) * kD + slice * kDpl;
-#pragma unroll
-            for (int g = 0; g < kG; ++g)
-#pragma unroll
-                for (int i = 0; i < kDpl; ++i) dst[g * kD + i] = acc[g][i];
+            if (col < kG) *reinterpret_cast<float4*>(reduce + (wave * kG + col) * kD + dt * 16 + quad * 4) = o;
         }
         __syncthreads();
 
-        const bool single = len <= kChunk || p.max_chunks <= 1;
+        const bool single = lens[cur.row] <= kChunk || p.max_chunks <= 1;
+        const std::uint32_t qh0 = cur.kvh * kG;
         for (int idx = tid; idx < kG * kD; idx += kThreads) {
             const int g = idx / kD, d = idx % kD;
             float m = -INFINITY;
@@ -747,13 +944,13 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             for (int w = 0; w < kWaves; ++w) {
                 const float f = exp2_shifted(wstats[w][2 * g], m);
                 l += wstats[w][2 * g + 1] * f;
-                sum += (reduce[(w * 2) * kG * kD + idx] + reduce[(w * 2 + 1) * kG * kD + idx]) * f;
+                sum += reduce[w * kG * kD + idx] * f;
             }
-            const std::uint64_t out_row = static_cast<std::uint64_t>(row) * p.query_heads + qh0 + g;
+            const std::uint64_t out_row = static_cast<std::uint64_t>(cur.row) * p.query_heads + qh0 + g;
             if (single) {
                 p.output[out_row * kD + d] = l > 0.0f ? sum / l : 0.0f;
             } else {
-                const std::uint64_t slot = out_row * p.max_chunks + chunk;
+                const std::uint64_t slot = out_row * p.max_chunks + cur.chunk;
                 p.partial_acc[slot * kD + d] = sum;
                 if (d == 0) {
                     p.partial_ml[2 * slot] = m;
@@ -761,34 +958,80 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
                 }
             }
         }
-        __syncthreads();  // LDS is reused by the next item
+        if (!has_next) break;
+        __syncthreads();  // reduce, wstats and qsplit[sel] are reused
+        item = next_item;
+        cur = nxt;
+        cur_pages = nxt_pages;
+        sel ^= 1;
     }
 }
 
 // Combines the chunk partials of every (row, query head) with more than one
-// chunk, in ascending chunk order.
-__global__ __launch_bounds__(64) void paged_attention_combine_kernel(Params p, std::uint32_t head_dim) {
+// chunk. One 128-thread block per (row, query head): the chunk weights
+// exp2(m_c - m) of 128 chunks at a time go to LDS, then every thread sums its
+// dimensions over those chunks with independent loads. All sums run in
+// ascending chunk order, so results are deterministic.
+constexpr int kCombineThreads = 128;
+constexpr int kCombineMaxD = 256;  // largest head_size of the kernels that write partials
+
+__global__ __launch_bounds__(kCombineThreads) void paged_attention_combine_kernel(Params p, std::uint32_t head_dim) {
+    __shared__ float weight[kCombineThreads];
+    __shared__ float wave_max_of[kCombineThreads / 64];
     const std::uint32_t row = p.row_base + blockIdx.x / p.query_heads;
     const std::uint32_t qh = blockIdx.x % p.query_heads;
     const std::uint64_t len = row_length(p, row);
     const std::uint64_t needed = (len + kChunk - 1) / kChunk;
     const std::uint32_t nchunks =
         needed < p.max_chunks ? static_cast<std::uint32_t>(needed) : p.max_chunks;
-    if (nchunks <= 1) return;
+    if (nchunks <= 1) return;  // uniform over the block
+    const int tid = threadIdx.x;
     const std::uint64_t out_row = static_cast<std::uint64_t>(row) * p.query_heads + qh;
     const float* ml = p.partial_ml + out_row * p.max_chunks * 2;
+    const float* acc = p.partial_acc + out_row * p.max_chunks * head_dim;
+
     float m = -INFINITY;
-    for (std::uint32_t c = 0; c < nchunks; ++c) m = fmaxf(m, ml[2 * c]);
+    for (std::uint32_t c = tid; c < nchunks; c += kCombineThreads) m = fmaxf(m, ml[2 * c]);
+    m = wave_max(m);
+    if (tid % 64 == 0) wave_max_of[tid / 64] = m;
+    __syncthreads();
+    m = fmaxf(wave_max_of[0], wave_max_of[1]);
+
+    constexpr int kDims = kCombineMaxD / kCombineThreads;
+    float o[kDims];
+#pragma unroll
+    for (int j = 0; j < kDims; ++j) o[j] = 0.0f;
     float l = 0.0f;
-    for (std::uint32_t c = 0; c < nchunks; ++c) l += ml[2 * c + 1] * exp2_shifted(ml[2 * c], m);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    for (std::uint32_t d = threadIdx.x; d < head_dim; d += 64) {
-        float o = 0.0f;
-        for (std::uint32_t c = 0; c < nchunks; ++c) {
-            o = fmaf(p.partial_acc[(out_row * p.max_chunks + c) * head_dim + d],
-                     exp2_shifted(ml[2 * c], m), o);
+    for (std::uint32_t c0 = 0; c0 < nchunks; c0 += kCombineThreads) {
+        const std::uint32_t n = nchunks - c0 < kCombineThreads ? nchunks - c0 : kCombineThreads;
+        __syncthreads();  // the previous tile's weights are no longer read
+        if (static_cast<std::uint32_t>(tid) < n) weight[tid] = exp2_shifted(ml[2 * (c0 + tid)], m);
+        __syncthreads();
+        for (std::uint32_t c = 0; c < n; ++c) l = fmaf(ml[2 * (c0 + c) + 1], weight[c], l);
+#pragma unroll
+        for (int j = 0; j < kDims; ++j) {
+            const std::uint32_t d = tid + kCombineThreads * j;
+            if (d < head_dim) {
+                const float* src = acc + static_cast<std::uint64_t>(c0) * head_dim + d;
+                float sum = o[j];
+                std::uint32_t c = 0;
+                for (; c + 8 <= n; c += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = src[static_cast<std::uint64_t>(c + u) * head_dim];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) sum = fmaf(v[u], weight[c + u], sum);
+                }
+                for (; c < n; ++c) sum = fmaf(src[static_cast<std::uint64_t>(c) * head_dim], weight[c], sum);
+                o[j] = sum;
+            }
         }
-        p.output[out_row * head_dim + d] = o * inv;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int j = 0; j < kDims; ++j) {
+        const std::uint32_t d = tid + kCombineThreads * j;
+        if (d < head_dim) p.output[out_row * head_dim + d] = o[j] * inv;
     }
 }
 
@@ -886,7 +1129,7 @@ int launch_split(Params p, std::uint64_t rows, std::uint64_t max_chunks, hipStre
         if (status != KVFLUX_OK) return status;
         if (max_chunks > 1) {
             hipLaunchKernelGGL(paged_attention_combine_kernel,
-                               dim3(static_cast<unsigned>(n * p.query_heads)), dim3(64), 0, s, p,
+                               dim3(static_cast<unsigned>(n * p.query_heads)), dim3(kCombineThreads), 0, s, p,
                                static_cast<std::uint32_t>(kD));
             status = launch_status("paged_attention_combine_kernel");
             if (status != KVFLUX_OK) return status;
@@ -939,7 +1182,7 @@ int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s) {
                                         ? p.num_rows - base : 0x7fffffffULL / p.query_heads;
             p.row_base = static_cast<std::uint32_t>(base);
             hipLaunchKernelGGL(paged_attention_combine_kernel, dim3(static_cast<unsigned>(n * p.query_heads)),
-                               dim3(64), 0, s, p, static_cast<std::uint32_t>(kD));
+                               dim3(kCombineThreads), 0, s, p, static_cast<std::uint32_t>(kD));
             status = launch_status("paged_attention_combine_kernel");
             if (status != KVFLUX_OK) return status;
         }
@@ -951,7 +1194,7 @@ template <typename E, int kD>
 int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint64_t max_chunks,
                    hipStream_t s) {
     if constexpr (!std::is_same<E, F32>::value && (kD == 64 || kD == 128)) {
-        if (p.block_size.divisor == 16 && rows <= kPlanRows) {
+        if (p.block_size.divisor == 16 && rows <= kPlanRows && p.width > 0) {
             switch (group) {
             case 1: return launch_bs16<E, kD, 1>(p, max_chunks, s);
             case 2: return launch_bs16<E, kD, 2>(p, max_chunks, s);
