@@ -88,6 +88,10 @@ def check(status: int) -> None:
         raise KvfluxError(status, lib().kvflux_last_error().decode())
 
 
+def last_error() -> str:
+    return lib().kvflux_last_error().decode()
+
+
 def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args))
 

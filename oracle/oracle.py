@@ -93,6 +93,20 @@ def decode(bits: np.ndarray, dtype: int) -> np.ndarray:
     return bf16_to_f32(bits) if dtype == BF16 else f16_to_f32(bits)
 
 
+def encode(values: np.ndarray, dtype: int) -> np.ndarray:
+    """FP32 values -> storage bits of `dtype`, rounding to nearest even (the
+    vectorised form of oracle_f32_to_bf16 / oracle_f32_to_f16)."""
+    values = np.asarray(values, dtype=np.float32)
+    if dtype == F32:
+        return values.copy()
+    if dtype == F16:
+        return values.astype(np.float16).view(np.uint16)
+    u = values.view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(values)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
+
+
 def np_dtype(dtype: int):
     return np.float32 if dtype == F32 else np.uint16
 

@@ -194,6 +194,9 @@ def test_bf16_and_f16_rounding():
     for x in xs:
         assert lib.oracle_f32_to_bf16(float(x)) == exact_bf16(x)
         assert lib.oracle_f32_to_f16(float(x)) == int(np.float16(x).view(np.uint16))
+    # the vectorised encoder agrees with the scalar ones
+    assert np.array_equal(oracle.encode(xs, oracle.BF16), [exact_bf16(x) for x in xs])
+    assert np.array_equal(oracle.encode(xs, oracle.F16), [lib.oracle_f32_to_f16(float(x)) for x in xs])
     halves = np.arange(2**16, dtype=np.uint32).astype(np.uint16)
     finite = halves[~np.isnan(halves.view(np.float16))]
     for h in finite[::61]:
