@@ -1,8 +1,8 @@
 // Causal paged prefill on MFMA (gfx950): BF16/FP16 caches, head_size 64/128.
 //
-// One workgroup (4 wavefronts) owns one kv head and a block of 256 rows,
+// One workgroup (8 wavefronts, two per SIMD) owns one kv head and a block of 256 rows,
 // a row being a (query token, query head) pair of that kv head's group:
-// 256 / G tokens x G heads. Wavefront w owns row blocks 4w .. 4w+3 of 16 rows
+// 256 / G tokens x G heads. Wavefront w owns row blocks 2w, 2w+1 of 16 rows
 // (row block b = head b % G, tokens 16 * (b / G) ..). Keys stream through
 // LDS in tiles of 64 (K and V, staged through registers so the next tile's
 // loads overlap this tile's MFMAs), processed as two halves of 32 keys:
@@ -30,13 +30,16 @@ typedef __attribute__((ext_vector_type(4))) float pf_f32x4_t;
 typedef short pf_i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pf_i16x4_t pf_lds_i16x4_t;
 
+typedef __attribute__((ext_vector_type(2))) float pf_f32x2_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 pf_bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 pf_f16x2_t;
+
+// pack(a, b): a in the low half, b in the high half, each rounded to nearest
+// even (one v_cvt_pk_{bf16,f16}_f32).
 struct PfBf16 {
     using Vec = pf_bf16x8_t;
-    __device__ static std::uint32_t round(float x) {  // RNE to BF16 (NaN stays NaN)
-        std::uint32_t u = __float_as_uint(x);
-        if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-        u += 0x7fffu + ((u >> 16) & 1u);
-        return u >> 16;
+    __device__ static std::uint32_t pack(float a, float b) {
+        return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_bf16x2_t));
     }
     __device__ static pf_f32x4_t mma(const Vec& a, const Vec& b, const pf_f32x4_t& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -44,17 +47,37 @@ struct PfBf16 {
 };
 struct PfF16 {
     using Vec = pf_f16x8_t;
-    __device__ static std::uint32_t round(float x) {
-        return __builtin_bit_cast(std::uint16_t, static_cast<_Float16>(x));
+    __device__ static std::uint32_t pack(float a, float b) {
+        return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_f16x2_t));
     }
     __device__ static pf_f32x4_t mma(const Vec& a, const Vec& b, const pf_f32x4_t& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
 };
 
-constexpr int kPfThreads = 256;
+// NaN-propagating maximum of three (one v_maximum3_f32).
+__device__ inline float max3(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+// Maximum over the four lanes l, l^16, l^32, l^48 (the four quads of a
+// column) with two cross-row lane swaps, no LDS round trip.
+__device__ inline float max_across_quads(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float sum_across_quads(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+constexpr int kPfThreads = 512;   // 8 wavefronts, two per SIMD
 constexpr int kPfWaves = kPfThreads / 64;
 constexpr int kPfRows = 256;      // rows per workgroup
+constexpr int kPfNt = kPfRows / 16 / kPfWaves;  // 16-row blocks per wavefront
 constexpr int kPfTile = 64;       // keys per LDS tile
 constexpr int kPfTableMax = 2048; // page ids held in LDS (kv_len <= 2048 * block_size)
 // Marks a missing page (table shorter than the tile, or an id >= num_blocks):
@@ -79,7 +102,7 @@ struct PrefillParams {
 };
 
 template <typename E, int kD, int kG>
-__global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams p) {
     using M = E;
     using Vec = typename M::Vec;
     constexpr int kSteps = kD / 32;            // K-dim steps of S^T
@@ -114,11 +137,11 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
     }
 
     // Q rows of this wave: B operands [row block][K step], already scaled.
-    Vec qb_op[4][kSteps];
-    std::uint32_t row_token[4];
+    Vec qb_op[kPfNt][kSteps];
+    std::uint32_t row_token[kPfNt];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        const int b = wave * 4 + n;
+    for (int n = 0; n < kPfNt; ++n) {
+        const int b = wave * kPfNt + n;
         const int g = b % kG;
         const std::uint32_t token = t0 + 16 * (b / kG) + col;
         row_token[n] = token;
@@ -132,7 +155,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
             std::uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                w[e] = M::round(v[2 * e] * p.scale_log2) | (M::round(v[2 * e + 1] * p.scale_log2) << 16);
+                w[e] = M::pack(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2);
             }
             qb_op[n][kk] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
         }
@@ -149,8 +172,10 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
         return kCpr == 16 ? (c ^ (row & 15)) : (c ^ ((row >> 1) & 7));
     };
     auto v_slot = [](int row, int c) { return c ^ (kVSwz * (row & 7)); };
-    uint4 kreg[kChunksPerThread], vreg[kChunksPerThread];
-    auto fetch = [&](std::uint32_t tile) {
+    struct Staged {
+        uint4 k[kChunksPerThread], v[kChunksPerThread];
+    };
+    auto fetch = [&](std::uint32_t tile, Staged& st) {
 #pragma unroll
         for (int i = 0; i < kChunksPerThread; ++i) {
             const int id = tid + kPfThreads * i;
@@ -160,23 +185,23 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
             if (page != kPfNoPage) {
                 const std::uint64_t off = static_cast<std::uint64_t>(page) * page_stride +
                                           kvh * head_stride + static_cast<std::uint64_t>(key & bs_mask) * kD + c * 8;
-                kreg[i] = *reinterpret_cast<const uint4*>(kc + off);
-                vreg[i] = *reinterpret_cast<const uint4*>(vc + off);
+                st.k[i] = *reinterpret_cast<const uint4*>(kc + off);
+                st.v[i] = *reinterpret_cast<const uint4*>(vc + off);
             } else {
-                kreg[i] = make_uint4(0, 0, 0, 0);
-                vreg[i] = make_uint4(0, 0, 0, 0);
+                st.k[i] = make_uint4(0, 0, 0, 0);
+                st.v[i] = make_uint4(0, 0, 0, 0);
             }
         }
     };
-    auto stage = [&]() {
+    auto stage = [&](const Staged& st) {
         char* kb = reinterpret_cast<char*>(ktile);
         char* vb = reinterpret_cast<char*>(vtile);
 #pragma unroll
         for (int i = 0; i < kChunksPerThread; ++i) {
             const int id = tid + kPfThreads * i;
             const int row = id / kCpr, c = id % kCpr;
-            *reinterpret_cast<uint4*>(kb + row * kRowBytes + k_slot(row, c) * 16) = kreg[i];
-            *reinterpret_cast<uint4*>(vb + row * kRowBytes + v_slot(row, c) * 16) = vreg[i];
+            *reinterpret_cast<uint4*>(kb + row * kRowBytes + k_slot(row, c) * 16) = st.k[i];
+            *reinterpret_cast<uint4*>(vb + row * kRowBytes + v_slot(row, c) * 16) = st.v[i];
         }
     };
     // Transposing V^T reads: lane (q, s) addresses key row 4q + s/4 (+16 for
@@ -188,30 +213,27 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
         v_read0 = r * kRowBytes + (v_slot(r, c) * 16) + (s % 2) * 8;
     }
 
-    pf_f32x4_t acc[kDt][4];
+    pf_f32x4_t acc[kDt][kPfNt];
 #pragma unroll
     for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) acc[dt][n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float run_max[4], run_sum[4];
+        for (int n = 0; n < kPfNt; ++n) acc[dt][n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float run_max[kPfNt], run_sum[kPfNt];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int n = 0; n < kPfNt; ++n) {
         run_max[n] = -INFINITY;
         run_sum[n] = 0.0f;
     }
     const std::uint32_t min_limit = past + t0;  // smallest causal limit of the block
 
-    fetch(0);
-    for (std::uint32_t tile = 0; tile < ntiles; ++tile) {
-        stage();
-        __syncthreads();
-        if (tile + 1 < ntiles) fetch(tile + 1);
+    // Tiles alternate between two register sets, loaded two tiles ahead.
+    auto compute_tile = [&](std::uint32_t tile) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const std::uint32_t k0 = tile * kPfTile + 32 * h;
             if (k0 > last_key) break;  // uniform
             // S^T for keys k0 .. k0+31: two 16-key tiles x 4 row blocks.
-            pf_f32x4_t s[2][4];
+            pf_f32x4_t s[2][kPfNt];
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
                 const int row = 32 * h + 16 * kt + col;
@@ -224,7 +246,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
                                                              k_slot(row, c) * 16));
                 }
 #pragma unroll
-                for (int n = 0; n < 4; ++n) {
+                for (int n = 0; n < kPfNt; ++n) {
                     pf_f32x4_t x = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int kk = 0; kk < kSteps; ++kk) x = M::mma(a[kk], qb_op[n][kk], x);
@@ -232,22 +254,19 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
                 }
             }
             const bool edge = k0 + 31 > min_limit;  // uniform: causal mask needed
-            Vec pb[4];
+            Vec pb[kPfNt];
 #pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                if (edge) {
-                    const std::uint32_t limit = past + row_token[n];
+            for (int n = 0; n < kPfNt; ++n) {
+                if (edge) {  // keys past the row's causal limit (select, no branch)
+                    const std::int32_t room = static_cast<std::int32_t>(past + row_token[n] - k0 - 4 * quad);
 #pragma unroll
                     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            if (k0 + 16 * kt + 4 * quad + r > limit) s[kt][n][r] = -INFINITY;
-                        }
+                        for (int r = 0; r < 4; ++r) s[kt][n][r] = 16 * kt + r > room ? -INFINITY : s[kt][n][r];
                 }
-                float tmax = fmaxf(fmaxf(fmaxf(s[0][n][0], s[0][n][1]), fmaxf(s[0][n][2], s[0][n][3])),
-                                   fmaxf(fmaxf(s[1][n][0], s[1][n][1]), fmaxf(s[1][n][2], s[1][n][3])));
-                tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-                tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+                float tmax = max3(max3(s[0][n][0], s[0][n][1], s[0][n][2]), max3(s[0][n][3], s[1][n][0], s[1][n][1]),
+                                  max3(s[1][n][2], s[1][n][3], -INFINITY));
+                tmax = max_across_quads(tmax);
                 const bool grow = tmax > run_max[n] + kLazy;
                 const float old = run_max[n];
                 if (grow) run_max[n] = tmax;
@@ -262,16 +281,14 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
                 float psum = 0.0f;
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt) {
-                    std::uint32_t bits[4];
+                    float e[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        bits[r] = M::round(__builtin_amdgcn_exp2f(s[kt][n][r] - ref));
-                        psum += std::is_same<M, PfBf16>::value
-                                    ? __uint_as_float(bits[r] << 16)
-                                    : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<std::uint16_t>(bits[r])));
+                        e[r] = __builtin_amdgcn_exp2f(s[kt][n][r] - ref);
+                        psum += e[r];
                     }
-                    w[2 * kt] = bits[0] | (bits[1] << 16);
-                    w[2 * kt + 1] = bits[2] | (bits[3] << 16);
+                    w[2 * kt] = M::pack(e[0], e[1]);
+                    w[2 * kt + 1] = M::pack(e[2], e[3]);
                 }
                 run_sum[n] += psum;
                 pb[n] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
@@ -287,20 +304,33 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_kernel(PrefillPar
                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off + 16 * kRowBytes));
                 const Vec a = __builtin_bit_cast(Vec, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-                for (int n = 0; n < 4; ++n) acc[dt][n] = M::mma(a, pb[n], acc[dt][n]);
+                for (int n = 0; n < kPfNt; ++n) acc[dt][n] = M::mma(a, pb[n], acc[dt][n]);
             }
         }
+    };
+    Staged set0, set1;
+    fetch(0, set0);
+    if (ntiles > 1) fetch(1, set1);
+    for (std::uint32_t tile = 0; tile < ntiles; tile += 2) {
+        stage(set0);
+        __syncthreads();
+        if (tile + 2 < ntiles) fetch(tile + 2, set0);
+        compute_tile(tile);
         __syncthreads();  // the tile is consumed before the next stage()
+        if (tile + 1 >= ntiles) break;
+        stage(set1);
+        __syncthreads();
+        if (tile + 3 < ntiles) fetch(tile + 3, set1);
+        compute_tile(tile + 1);
+        __syncthreads();
     }
 
     // Row sums across the four quads, then O = O^T / l.
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        float l = run_sum[n];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+    for (int n = 0; n < kPfNt; ++n) {
+        const float l = sum_across_quads(run_sum[n]);
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        const int b = wave * 4 + n;
+        const int b = wave * kPfNt + n;
         const int g = b % kG;
         const std::uint32_t token = row_token[n];
         if (token < t_end) {
