@@ -5,18 +5,19 @@
 //   out[((off + t) * H + h) * D + d] = cache[((table[t / bs] * H + h) * bs + t % bs) * D + d]
 // for K and V, generalised to many sequences per launch.
 //
-// gfx950 mapping: one workgroup per (logical page, sequence). A page of one
-// cache is H*bs*D elements stored contiguously, so the workgroup streams it
-// with consecutive lanes on consecutive 16-byte vectors (fully coalesced
-// reads); each (head, token) row lands as one contiguous row of the output.
-// Only the valid tokens of the tail page are touched. Every thread issues
-// all of its K and V loads before its stores.
+// gfx950 mapping: one 512-thread workgroup per (logical page, sequence,
+// cache): blockIdx.z selects K (0) or V (1). A page of one cache is H*bs*D
+// elements stored contiguously, so the workgroup streams it with consecutive
+// lanes on consecutive 16-byte vectors (fully coalesced reads); each
+// (head, token) row lands as one contiguous row of the output. Only the
+// valid tokens of the tail page are touched. Every thread issues all of its
+// loads before its stores.
 #include "common.h"
 
 namespace kvflux_hip {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 
 template <typename Vec, int kMaxPerThread>
 __global__ __launch_bounds__(kThreads) void paged_kv_gather_kernel(
@@ -27,21 +28,25 @@ __global__ __launch_bounds__(kThreads) void paged_kv_gather_kernel(
     Vec* __restrict__ value_out, std::uint32_t seq_base, FastDiv vectors_per_row,
     FastDiv block_size, std::uint32_t heads, std::uint32_t page_vectors) {
     const std::uint32_t seq = seq_base + blockIdx.y;
-    const std::uint64_t logical = blockIdx.x;
-    const std::uint64_t length = seq_lens[seq];
-    const std::uint64_t first_token = logical * block_size.divisor;
-    if (first_token >= length || logical >= table_width) return;
+    const std::uint64_t logical = blockIdx.x;  // < table_width (grid.x <= width)
+    // The three metadata loads are independent: issue them together.
     const std::uint64_t page = block_table[seq * table_width + logical];
+    const std::uint64_t length = seq_lens[seq];
+    const std::uint64_t out_first = out_offsets[seq];
+    const std::uint64_t first_token = logical * block_size.divisor;
+    if (first_token >= length) return;
     if (page >= num_blocks) return;  // padding or corrupt id: never dereference
     const std::uint64_t remaining = length - first_token;
     const std::uint32_t valid =
         remaining < block_size.divisor ? static_cast<std::uint32_t>(remaining) : block_size.divisor;
 
     const std::uint64_t src_base = page * page_vectors;
-    const std::uint64_t out_token = out_offsets[seq] + first_token;
+    const std::uint64_t out_token = out_first + first_token;
     const std::uint32_t vpr = vectors_per_row.divisor;
 
-    Vec k[kMaxPerThread], v[kMaxPerThread];
+    const Vec* __restrict__ src = blockIdx.z == 0 ? key_cache : value_cache;
+    Vec* __restrict__ out = blockIdx.z == 0 ? key_out : value_out;
+    Vec k[kMaxPerThread];
     std::uint64_t dst[kMaxPerThread];
     bool live[kMaxPerThread];
 #pragma unroll
@@ -53,21 +58,16 @@ __global__ __launch_bounds__(kThreads) void paged_kv_gather_kernel(
         const std::uint32_t token = row - head * block_size.divisor;
         live[u] = i < page_vectors && token < valid;
         dst[u] = ((out_token + token) * heads + head) * vpr + col;
-        if (live[u]) {
-            k[u] = key_cache[src_base + i];
-            v[u] = value_cache[src_base + i];
-        }
+        if (live[u]) k[u] = src[src_base + i];
     }
 #pragma unroll
     for (int u = 0; u < kMaxPerThread; ++u) {
-        if (live[u]) {
-            key_out[dst[u]] = k[u];
-            value_out[dst[u]] = v[u];
-        }
+        if (live[u]) out[dst[u]] = k[u];
     }
 }
 
-// Pages larger than kThreads * 16 vectors: the same mapping in a loop.
+// Pages larger than kThreads * 16 vectors: the same mapping in a loop
+// (blockIdx.z selects the cache as above).
 template <typename Vec>
 __global__ __launch_bounds__(kThreads) void paged_kv_gather_kernel_loop(
     const Vec* __restrict__ key_cache, const Vec* __restrict__ value_cache,
@@ -90,8 +90,11 @@ __global__ __launch_bounds__(kThreads) void paged_kv_gather_kernel_loop(
         const std::uint64_t head = row / block_size, token = row % block_size;
         if (token >= valid) continue;
         const std::uint64_t d = ((out_token + token) * heads + head) * vpr + col;
-        key_out[d] = key_cache[page * page_vectors + i];
-        value_out[d] = value_cache[page * page_vectors + i];
+        if (blockIdx.z == 0) {
+            key_out[d] = key_cache[page * page_vectors + i];
+        } else {
+            value_out[d] = value_cache[page * page_vectors + i];
+        }
     }
 }
 
@@ -108,7 +111,7 @@ int launch(const void* kc, const void* vc, std::uint64_t num_blocks, std::uint64
     if (pages > 0x7fffffffULL) return fail(KVFLUX_ERR_UNSUPPORTED, "gather: too many pages");
     for (std::uint64_t base = 0; base < num_seqs; base += 65535) {
         const std::uint64_t n = num_seqs - base < 65535 ? num_seqs - base : 65535;
-        const dim3 grid(static_cast<unsigned>(pages), static_cast<unsigned>(n));
+        const dim3 grid(static_cast<unsigned>(pages), static_cast<unsigned>(n), 2);
         if (page_vectors <= kThreads * 4) {
             hipLaunchKernelGGL((paged_kv_gather_kernel<Vec, 4>), grid, dim3(kThreads), 0, s,
                                static_cast<const Vec*>(kc), static_cast<const Vec*>(vc),

@@ -8,15 +8,18 @@
 // `row_bytes / W` vectors of W bytes (W = 16 when the row and the four base
 // pointers allow it, i.e. global_load/store_dwordx4). Consecutive lanes take
 // consecutive vectors of one row, so a wavefront reads 1 KiB of contiguous
-// input and writes whole 256-byte rows (D=128, BF16). Each thread moves
-// UNROLL vectors of K and of V with all loads issued before the stores.
+// input and writes whole 256-byte rows (D=128, BF16). Each thread moves one
+// vector of K and one of V: the many short-lived workgroups (512 threads)
+// keep more independent slot and row loads in flight than fewer threads
+// moving several vectors each (measured on MI355X: 5.3 us against 20.8 us
+// for 4096 tokens x 8 heads x 128 BF16).
 #include "common.h"
 
 namespace kvflux_hip {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kThreads = 512;
+constexpr int kUnroll = 1;
 
 template <typename Vec>
 __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel(
