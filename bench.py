@@ -14,8 +14,16 @@ Also measured in the same run (sub-objects of the JSON line):
   write  : slot-mapped KV write, 4096 tokens x 8 heads x 128, BF16, 65536-page pool
   gather : BlockTable gather, 64 sequences with L ~ U[512, 8192], H=8, D=128,
            FP16 and BF16, odd pages of a full 65536-page pool
+  prefill: causal paged prefill on MFMA, 8 sequences x 4096 tokens written
+           through slot_mapping into random pages, 32 q / 8 kv heads, D=128,
+           BF16; TFLOP/s and MFMA utilisation against 2.5 PFLOP/s dense BF16
   cpu_baseline : the CPU oracle (gather + double-precision attention, one
            thread) on a bounded sample of the decode rows, timed here.
+
+roofline.traffic is the HBM traffic of one decode call measured with
+rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by what the same counters read
+for a copy of known size (`python bench.py --calibrate-copy`); it is read
+from profiles/decode_bs16_traffic.txt when that summary is present.
 
 Every timed region launches through the C ABI on a dedicated stream with all
 inputs and metadata already resident in HBM; HIP events on that stream give
@@ -37,6 +45,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
+TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_bs16_traffic.txt"
 METRIC = "decode paged-attn HBM TB/s (% of peak) + KV write/gather GB/s, 1 GPU"
 
 
@@ -164,7 +174,8 @@ def bench_decode(v2, args, stream):
         "flops": flops,
         "sum_len": int(lens.sum()),
         "max_abs_err": err,
-        "cpu": {"value": cpu_bytes / cpu_s / 1e12, "unit": "TB/s", "cores": 1, "kind": "port",
+        "cpu": None if not sample_rows else
+               {"value": cpu_bytes / cpu_s / 1e12, "unit": "TB/s", "cores": 1, "kind": "port",
                 "seconds": cpu_s,
                 "sample": f"{len(sample_rows)} decode rows (L={[int(lens[r]) for r in sample_rows]}, "
                           "32 q heads each): page gather + double-precision softmax attention, 1 thread"},
@@ -299,15 +310,113 @@ def bench_gather(v2, args, stream, dtype_name: str):
             "bytes": bytes_step, "tokens": total, "mismatched_elements_sampled": mism}
 
 
+# --------------------------------------------------------------------- prefill
+def bench_prefill(v2, args, stream):
+    from kvflux_amd import capi, device
+    from oracle import oracle
+
+    S, T, H, Hq, D, bs = 8, 4096, 8, 32, 128, 16
+    rng = np.random.default_rng(args.seed + 30)
+    pool = v2.PhysicalBlockPool(S * T // bs + 256, bs)
+    storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
+    fragment_pool(pool, rng.permutation(pool.capacity()))
+    seqs, tables, qs = [], [], []
+    kn, vn = device.DeviceBuffer(T * H * D * 2), device.DeviceBuffer(T * H * D * 2)
+    for i in range(S):
+        s = v2.SequenceState(i, pool)
+        s.append_tokens(T)
+        seqs.append(s)
+        device.fill_random(kn.ptr, T * H * D, capi.DTYPE_BF16, 1, args.seed + 31 + 2 * i)
+        device.fill_random(vn.ptr, T * H * D, capi.DTYPE_BF16, 1, args.seed + 32 + 2 * i)
+        v2.write_paged_kv(storage, kn.ptr, vn.ptr, v2.build_slot_mapping([(s, t) for t in range(T)]))
+        tables.append(device.to_device(np.array(v2.build_read_block_table(s), np.uint64)))
+        q = device.DeviceBuffer(T * Hq * D * 4)
+        device.fill_random(q.ptr, T * Hq * D, capi.DTYPE_F32, 1, args.seed + 50 + i)
+        qs.append(q)
+    out = device.DeviceBuffer(S * T * Hq * D * 4)
+    lib = capi.lib()
+    kb, vb = storage.key_base(), storage.value_base()
+    npages = T // bs
+
+    def launch():
+        for i in range(S):
+            capi.check(lib.kvflux_paged_prefill(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16, tables[i].ptr,
+                                                npages, T, T, Hq, qs[i].ptr, out.ptr + i * T * Hq * D * 4, stream))
+
+    ms = time_launches(launch, stream, max(1, args.warmup // 2), max(3, args.steps // 4))
+    flops = S * T * (T + 1) / 2 * Hq * D * 4
+    # The last queries (longest rows) of the first and last sequence against the CPU reference.
+    page_bytes = H * bs * D * 2
+    err = 0.0
+    checked = 0
+    for i in (0, S - 1):
+        ids = device.memcpy_d2h(tables[i].ptr, npages * 8, np.uint64)
+        kc = np.concatenate([device.memcpy_d2h(kb + int(p) * page_bytes, page_bytes, np.uint16) for p in ids])
+        vc = np.concatenate([device.memcpy_d2h(vb + int(p) * page_bytes, page_bytes, np.uint16) for p in ids])
+        tail = 2
+        qh = device.memcpy_d2h(qs[i].ptr + (T - tail) * Hq * D * 4, tail * Hq * D * 4, np.float32)
+        ref = oracle.paged_attention_causal(kc, vc, H, bs, D, oracle.BF16, np.arange(npages, dtype=np.uint64), T, qh,
+                                            tail, Hq, threads=8)
+        got = device.memcpy_d2h(out.ptr + (i * T + T - tail) * Hq * D * 4, tail * Hq * D * 4, np.float32)
+        err = max(err, float(np.abs(got - ref).max()))
+        checked += tail
+    del seqs
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "8 x 4096-token causal prefill, 32 q / 8 kv heads, D=128, BF16 KV, block_size 16",
+            "kernel": "paged_prefill_kernel<bf16,128,4>", "ms": ms, "TFLOPs": tflops,
+            "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS, "flops": flops,
+            "max_abs_err_vs_oracle": err, "rows_checked": checked, "tolerance": 2e-2}
+
+
+def calibrate_copy(args) -> int:
+    """A plain 1 GiB device-to-device copy (the runtime's copy kernel), run
+    under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE to scale those counters."""
+    from kvflux_amd import capi, device
+    capi.call("kvflux_set_device", 0)
+    n = 1 << 30
+    a, b = device.DeviceBuffer(n), device.DeviceBuffer(n)
+    a.fill(1)
+    b.fill(0)
+    device.synchronize()
+    for _ in range(5):
+        capi.call("kvflux_memcpy_async", C.c_void_p(b.ptr), C.c_void_p(a.ptr), n, None)
+    device.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read_per_dispatch": n, "bytes_written_per_dispatch": n}))
+    return 0
+
+
+def read_traffic():
+    """HBM bytes per decode call from the committed rocprofv3 summary, or None."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    vals = {}
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            try:
+                vals[k.strip()] = float(v.split()[0])
+            except (ValueError, IndexError):
+                pass
+    need = ("decode_fetch_kib_per_call", "decode_write_kib_per_call", "copy_fetch_kib_per_gib", "copy_write_kib_per_gib")
+    if not all(k in vals for k in need):
+        return None
+    fetch = vals["decode_fetch_kib_per_call"] * (1 << 30) / vals["copy_fetch_kib_per_gib"]
+    write = vals["decode_write_kib_per_call"] * (1 << 30) / vals["copy_write_kib_per_gib"]
+    return int(fetch + write)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=2024)
-    ap.add_argument("--cpu-rows", type=int, default=2)
+    ap.add_argument("--cpu-rows", type=int, default=24, help="decode rows timed on the CPU oracle")
     ap.add_argument("--skip-aux", action="store_true", help="decode only")
+    ap.add_argument("--calibrate-copy", action="store_true", help="1 GiB device copy for counter scaling")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}); run with --gpus 1.", file=sys.stderr)
@@ -338,6 +447,11 @@ def main() -> int:
             log(f"gather {name} ...")
             aux[f"gather_{name}"] = bench_gather(v2, args, stream.handle, name)
             log(f"gather {aux[f'gather_{name}']}")
+        log("prefill ...")
+        aux["prefill"] = bench_prefill(v2, args, stream.handle)
+        log(f"prefill {aux['prefill']}")
+        for key in ("write", "gather_BFloat16", "gather_Float16"):
+            aux[key]["pct_of_peak"] = round(100 * aux[key]["GBps"] / PEAK_HBM_GBPS, 2)
 
     s = dec["ms"] * 1e-3
     achieved = dec["unique_bytes"] / s / 1e9
@@ -371,8 +485,9 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": None,
-            "kernel": "paged_attention_split_kernel<Bf16,128,4>",
+            "traffic": read_traffic(),
+            "kernel": "paged_decode_bs16_kernel<Bf16,128,4> (+ paged_attention_combine_kernel, "
+                      "both inside the timed kvflux_paged_attention call)",
             "bytes_per_launch": dec["unique_bytes"],
         },
         "cpu_baseline": dec["cpu"],
