@@ -15,6 +15,7 @@
 #include "kvflux/v2/paged_attention.h"
 #include "kvflux/v2/paged_kv_read.h"
 #include "kvflux/v2/paged_kv_write.h"
+#include "kvflux/v2/reference_attention.h"
 
 #include <cstdint>
 #include <stdexcept>
@@ -257,6 +258,19 @@ PYBIND11_MODULE(_kvflux, m) {
     }, py::arg("storage"), py::arg("sequence"), py::arg("query"), py::arg("output"),
        py::arg("query_tokens"), py::arg("query_heads"),
        py::arg("precision") = AttentionPrecision::Auto);
+    py::class_<AttentionShape>(m, "AttentionShape")
+        .def(py::init([](std::size_t qt, std::size_t kt, std::size_t qh, std::size_t kh, std::size_t d) {
+                 return AttentionShape{qt, kt, qh, kh, d};
+             }),
+             py::arg("query_tokens"), py::arg("kv_tokens"), py::arg("query_heads"), py::arg("kv_heads"),
+             py::arg("head_size"))
+        .def_readwrite("query_tokens", &AttentionShape::query_tokens)
+        .def_readwrite("kv_tokens", &AttentionShape::kv_tokens)
+        .def_readwrite("query_heads", &AttentionShape::query_heads)
+        .def_readwrite("kv_heads", &AttentionShape::kv_heads)
+        .def_readwrite("head_size", &AttentionShape::head_size);
+    m.def("reference_attention", &reference_attention, py::arg("query"), py::arg("key"), py::arg("value"),
+          py::arg("shape"));
     m.def("paged_attention_batch", [](const PagedKVStorage& s,
                                       const std::vector<const SequenceState*>& seqs,
                                       std::uintptr_t q, std::uintptr_t o, std::size_t query_heads) {
