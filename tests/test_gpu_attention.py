@@ -194,3 +194,62 @@ def test_c_abi_attention_and_errors(gpu):
                                       1000, 2, Hq, qd.ptr, od.ptr, wd.ptr, ws.value, None) == capi.ERR_INVALID
     assert lib.kvflux_paged_attention(kc.ptr, vc.ptr, blocks, H, bs, D, capi.DTYPE_BF16, td.ptr, 63, ld.ptr,
                                       1000, 2, 7, qd.ptr, od.ptr, wd.ptr, ws.value, None) == capi.ERR_INVALID
+
+
+SHARED_CASES = [  # name, kv_heads, q_heads, head_size
+    ("BFloat16", 2, 8, 128),
+    ("Float16", 2, 4, 64),
+    ("BFloat16", 1, 8, 64),
+    ("BFloat16", 4, 4, 128),
+]
+
+
+@pytest.mark.parametrize("name,kv_heads,q_heads,head_size", SHARED_CASES)
+def test_shared_full_chunks_mixed_batch(gpu, v2, name, kv_heads, q_heads, head_size):
+    """Rows that share whole 512-token chunks (two different prefixes), rows
+    equal to the prefix, unshared rows and a short row, in shuffled order:
+    the shared-prefix stage and the main kernel together match the oracle."""
+    bs = 16
+    cap = 1200
+    pool = v2.PhysicalBlockPool(cap, bs)
+    storage = v2.PagedKVStorage(pool, kv_heads, head_size, getattr(v2.DType, name))
+    rng = np.random.default_rng(77)
+    holders = [pool.allocate() for _ in range(cap)]
+    for idx in rng.permutation(cap)[::-1]:
+        pool.free(holders[idx])
+    base_a = v2.SequenceState(10**6, pool)
+    base_a.append_tokens(1536)
+    base_b = v2.SequenceState(10**6 + 1, pool)
+    base_b.append_tokens(1024)
+    seqs = []
+    plan = [("a", 1536), ("a", 1600), ("own", 700), ("a", 3000), ("b", 1100), ("own", 2048), ("a", 5000),
+            ("b", 2500), ("own", 100), ("a", 1537)]
+    order = rng.permutation(len(plan))
+    for i in order.tolist():
+        kind, L = plan[i]
+        if kind == "own":
+            s = v2.SequenceState(i, pool)
+            s.append_tokens(L)
+        else:
+            base, P = (base_a, 1536) if kind == "a" else (base_b, 1024)
+            s = base.fork_shared(i)
+            s.append_tokens(L - P)
+        seqs.append(s)
+    code = DTYPES[name][0]
+    n = storage.layout().cache_bytes() // storage.layout().element_bytes()
+    device.fill_random(storage.key_base(), n, code, 1, 5)
+    device.fill_random(storage.value_base(), n, code, 1, 6)
+    q = oracle.random_elements(0, len(seqs) * q_heads * head_size, oracle.F32, 1, 7)
+    qd = buffer_like(q)
+    od = buffer_like(np.zeros(q.size, np.float32))
+    v2.paged_attention_batch(storage, seqs, qd.ptr, od.ptr, q_heads)
+    got = od.download(np.float32)
+    kc, vc = host_cache(storage, name)
+    t = v2.build_batch_block_table(seqs)
+    expected = oracle.paged_attention_rows(kc, vc, kv_heads, bs, head_size, code,
+                                           np.array(t.block_table(), np.uint64), t.max_blocks_per_sequence(),
+                                           t.sequence_lengths(), q, q_heads, threads=8)
+    assert np.abs(got - expected).max() < TOL
+    od2 = buffer_like(np.zeros(q.size, np.float32))
+    v2.paged_attention_batch(storage, seqs, qd.ptr, od2.ptr, q_heads)
+    assert np.array_equal(od2.download(np.float32).view(np.uint32), got.view(np.uint32))
