@@ -38,6 +38,7 @@ typedef __attribute__((ext_vector_type(2))) _Float16 pf_f16x2_t;
 // even (one v_cvt_pk_{bf16,f16}_f32).
 struct PfBf16 {
     using Vec = pf_bf16x8_t;
+    static constexpr std::uint32_t kOnes = 0x3f803f80u;  // two 1.0
     __device__ static std::uint32_t pack(float a, float b) {
         return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_bf16x2_t));
     }
@@ -47,6 +48,7 @@ struct PfBf16 {
 };
 struct PfF16 {
     using Vec = pf_f16x8_t;
+    static constexpr std::uint32_t kOnes = 0x3c003c00u;  // two 1.0
     __device__ static std::uint32_t pack(float a, float b) {
         return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_f16x2_t));
     }
@@ -67,12 +69,6 @@ __device__ inline float max_across_quads(float x) {
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
-__device__ inline float sum_across_quads(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 
 constexpr int kPfThreads = 512;   // 8 wavefronts, two per SIMD
 constexpr int kPfWaves = kPfThreads / 64;
@@ -80,9 +76,9 @@ constexpr int kPfRows = 256;      // rows per workgroup
 constexpr int kPfNt = kPfRows / 16 / kPfWaves;  // 16-row blocks per wavefront
 constexpr int kPfTile = 64;       // keys per LDS tile
 constexpr int kPfTableMax = 2048; // page ids held in LDS (kv_len <= 2048 * block_size)
-// Marks a missing page (table shorter than the tile, or an id >= num_blocks):
-// its K and V read as zeros.
-constexpr std::uint32_t kPfNoPage = 0xffffffffu;
+// Flag bit of a missing page in the LDS page list (ids are below 2^31): it is
+// loaded from page 0 (never out of bounds) and its K and V staged as zeros.
+constexpr std::uint32_t kPfMissing = 0x80000000u;
 
 struct PrefillParams {
     const void* key_cache;
@@ -131,9 +127,14 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     const std::uint32_t last_key = past + t_end - 1;
     const std::uint32_t ntiles = last_key / kPfTile + 1;
     const std::uint32_t npages = ((ntiles * kPfTile - 1) >> p.bs_shift) + 1;
+    // Page ids of the tiles; a missing page (past the table or kv_len, or an
+    // id >= num_blocks) is loaded from page 0 and zeroed before it reaches LDS.
+    bool missing = false;
     for (std::uint32_t i = tid; i < npages; i += kPfThreads) {
-        const std::uint64_t id = i < p.table_len ? p.table[i] : kPfNoPage;
-        pages[i] = id < p.num_blocks ? static_cast<std::uint32_t>(id) : kPfNoPage;  // never dereferenced
+        const std::uint64_t id = i < p.table_len ? p.table[i] : p.num_blocks;
+        const bool ok = id < p.num_blocks && (static_cast<std::uint64_t>(i) << p.bs_shift) < p.kv_len;
+        pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
+        missing |= !ok && (static_cast<std::uint64_t>(i) << p.bs_shift) < p.kv_len;
     }
 
     // Q rows of this wave: B operands [row block][K step], already scaled.
@@ -160,14 +161,26 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             qb_op[n][kk] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
         }
     }
-    __syncthreads();  // pages[] ready
+    // pages[] ready; uniform: some page inside kv_len is missing
+    const bool table_gaps = __syncthreads_or(missing);
 
     // Tile staging: chunk id = tid + kPfThreads * i; row = id / kCpr, c = id % kCpr.
-    const std::uint16_t* kc = static_cast<const std::uint16_t*>(p.key_cache);
-    const std::uint16_t* vc = static_cast<const std::uint16_t*>(p.value_cache);
-    const std::uint64_t head_stride = static_cast<std::uint64_t>(kD) << p.bs_shift;
-    const std::uint64_t page_stride = head_stride * p.heads;
-    const std::uint32_t bs_mask = (1u << p.bs_shift) - 1;
+    // A tile starts on a page boundary (block_size divides 64), so a thread's
+    // row sits at a fixed offset in its page, and its page is entry
+    // tile * (64 / block_size) + row / block_size of pages[].
+    const char* kc = static_cast<const char*>(p.key_cache);
+    const char* vc = static_cast<const char*>(p.value_cache);
+    const std::uint32_t page_bytes = (static_cast<std::uint32_t>(kRowBytes) << p.bs_shift) * p.heads;
+    const std::uint32_t tile_pages_shift = 6 - p.bs_shift;
+    std::uint32_t lane_bytes[kChunksPerThread], row_page[kChunksPerThread];
+#pragma unroll
+    for (int i = 0; i < kChunksPerThread; ++i) {
+        const int id = tid + kPfThreads * i;
+        const int row = id / kCpr, c = id % kCpr;
+        row_page[i] = static_cast<std::uint32_t>(row) >> p.bs_shift;
+        lane_bytes[i] = ((kvh << p.bs_shift) + (static_cast<std::uint32_t>(row) & ((1u << p.bs_shift) - 1))) *
+                            kRowBytes + c * 16;
+    }
     auto k_slot = [](int row, int c) {  // conflict-free for 16-row ds_read_b128
         return kCpr == 16 ? (c ^ (row & 15)) : (c ^ ((row >> 1) & 7));
     };
@@ -175,25 +188,32 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     struct Staged {
         uint4 k[kChunksPerThread], v[kChunksPerThread];
     };
+    // Unconditional loads (straight-line code keeps the wait counts exact).
     auto fetch = [&](std::uint32_t tile, Staged& st) {
 #pragma unroll
         for (int i = 0; i < kChunksPerThread; ++i) {
-            const int id = tid + kPfThreads * i;
-            const int row = id / kCpr, c = id % kCpr;
-            const std::uint32_t key = tile * kPfTile + row;
-            const std::uint32_t page = key < p.kv_len ? pages[key >> p.bs_shift] : kPfNoPage;
-            if (page != kPfNoPage) {
-                const std::uint64_t off = static_cast<std::uint64_t>(page) * page_stride +
-                                          kvh * head_stride + static_cast<std::uint64_t>(key & bs_mask) * kD + c * 8;
-                st.k[i] = *reinterpret_cast<const uint4*>(kc + off);
-                st.v[i] = *reinterpret_cast<const uint4*>(vc + off);
-            } else {
-                st.k[i] = make_uint4(0, 0, 0, 0);
-                st.v[i] = make_uint4(0, 0, 0, 0);
-            }
+            const std::uint32_t page = pages[(tile << tile_pages_shift) + row_page[i]] & ~kPfMissing;
+            const std::uint64_t off = static_cast<std::uint64_t>(page) * page_bytes + lane_bytes[i];
+            st.k[i] = *reinterpret_cast<const uint4*>(kc + off);
+            st.v[i] = *reinterpret_cast<const uint4*>(vc + off);
         }
     };
-    auto stage = [&](const Staged& st) {
+    auto stage = [&](std::uint32_t tile, Staged& st) {
+        // Keys at or past kv_len, or on a missing page, are staged as zeros
+        // (finite V under a zero weight). Uniform test: only the last tile or
+        // a table with gaps takes it.
+        if (table_gaps || (tile + 1) * kPfTile > p.kv_len) {
+#pragma unroll
+            for (int i = 0; i < kChunksPerThread; ++i) {
+                const int row = (tid + kPfThreads * i) / kCpr;
+                const std::uint32_t key = tile * kPfTile + row;
+                const bool zero = key >= p.kv_len || (pages[(tile << tile_pages_shift) + row_page[i]] & kPfMissing);
+                if (zero) {
+                    st.k[i] = make_uint4(0, 0, 0, 0);
+                    st.v[i] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
         char* kb = reinterpret_cast<char*>(ktile);
         char* vb = reinterpret_cast<char*>(vtile);
 #pragma unroll
@@ -205,25 +225,41 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         }
     };
     // Transposing V^T reads: lane (q, s) addresses key row 4q + s/4 (+16 for
-    // the second half of the operand), dims 16*dt + 4*(s%4).
-    std::uint32_t v_read0;
+    // the second half of the operand), dims 16*dt + 4*(s%4). The swizzle
+    // acts on bits 4..6 of the byte offset and dt on bits 5..7, so block dt
+    // is v_read0 ^ (dt << 5); row offsets of whole tiles are immediates.
+    std::uint32_t v_rd[kDt];
     {
         const int s = lane % 16, r = 4 * quad + s / 4;
         const int c = (4 * (s % 4)) / 8;
-        v_read0 = r * kRowBytes + (v_slot(r, c) * 16) + (s % 2) * 8;
+        const std::uint32_t v_read0 = r * kRowBytes + (v_slot(r, c) * 16) + (s % 2) * 8;
+#pragma unroll
+        for (int dt = 0; dt < kDt; ++dt) v_rd[dt] = v_read0 ^ (dt << 5);
     }
+    // K A operand of lane (quad, col) for step kk: key row 16*m + col (the
+    // K swizzle depends on the row only through col), 16-byte column
+    // quad + 4*kk.
+    std::uint32_t k_rd[kSteps];
+#pragma unroll
+    for (int kk = 0; kk < kSteps; ++kk) k_rd[kk] = col * kRowBytes + k_slot(col, quad + 4 * kk) * 16;
 
     pf_f32x4_t acc[kDt][kPfNt];
 #pragma unroll
     for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
         for (int n = 0; n < kPfNt; ++n) acc[dt][n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float run_max[kPfNt], run_sum[kPfNt];
+    // Per row block: the row sums of the rounded weights (an MFMA against a
+    // matrix of ones, so every entry holds its column's sum) and minus the
+    // row's reference point, broadcast: the S^T accumulators start from it,
+    // so the scores arrive already shifted.
+    pf_f32x4_t lsum[kPfNt], nref[kPfNt];
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
-        run_max[n] = -INFINITY;
-        run_sum[n] = 0.0f;
+        lsum[n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        nref[n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    bool have_ref = false;  // uniform: false until the first half-tile sets every row's reference
+    const Vec ones = __builtin_bit_cast(Vec, make_uint4(M::kOnes, M::kOnes, M::kOnes, M::kOnes));
     const std::uint32_t min_limit = past + t0;  // smallest causal limit of the block
 
     // Tiles alternate between two register sets, loaded two tiles ahead.
@@ -232,73 +268,80 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         for (int h = 0; h < 2; ++h) {
             const std::uint32_t k0 = tile * kPfTile + 32 * h;
             if (k0 > last_key) break;  // uniform
-            // S^T for keys k0 .. k0+31: two 16-key tiles x 4 row blocks.
+            // S^T - ref for keys k0 .. k0+31: two 16-key tiles x the row blocks.
             pf_f32x4_t s[2][kPfNt];
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                const int row = 32 * h + 16 * kt + col;
                 Vec a[kSteps];
 #pragma unroll
                 for (int kk = 0; kk < kSteps; ++kk) {
-                    const int c = quad + 4 * kk;
                     a[kk] = __builtin_bit_cast(
-                        Vec, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(ktile) + row * kRowBytes +
-                                                             k_slot(row, c) * 16));
+                        Vec, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(ktile) +
+                                                             (32 * h + 16 * kt) * kRowBytes + k_rd[kk]));
                 }
 #pragma unroll
                 for (int n = 0; n < kPfNt; ++n) {
-                    pf_f32x4_t x = {0.0f, 0.0f, 0.0f, 0.0f};
+                    pf_f32x4_t x = nref[n];
 #pragma unroll
                     for (int kk = 0; kk < kSteps; ++kk) x = M::mma(a[kk], qb_op[n][kk], x);
                     s[kt][n] = x;
                 }
             }
-            const bool edge = k0 + 31 > min_limit;  // uniform: causal mask needed
-            Vec pb[kPfNt];
+            if (k0 + 31 > min_limit) {  // uniform; keys past the row's causal limit
 #pragma unroll
-            for (int n = 0; n < kPfNt; ++n) {
-                if (edge) {  // keys past the row's causal limit (select, no branch)
+                for (int n = 0; n < kPfNt; ++n) {
                     const std::int32_t room = static_cast<std::int32_t>(past + row_token[n] - k0 - 4 * quad);
 #pragma unroll
                     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) s[kt][n][r] = 16 * kt + r > room ? -INFINITY : s[kt][n][r];
                 }
-                float tmax = max3(max3(s[0][n][0], s[0][n][1], s[0][n][2]), max3(s[0][n][3], s[1][n][0], s[1][n][1]),
-                                  max3(s[1][n][2], s[1][n][3], -INFINITY));
-                tmax = max_across_quads(tmax);
-                const bool grow = tmax > run_max[n] + kLazy;
-                const float old = run_max[n];
-                if (grow) run_max[n] = tmax;
-                const float ref = run_max[n] == -INFINITY ? 0.0f : run_max[n];
-                if (grow && old != -INFINITY) {
-                    const float alpha = __builtin_amdgcn_exp2f(old - ref);
-                    run_sum[n] *= alpha;
+            }
+            // Row maxima relative to the reference (equal in the four quads of a column).
+            float tmax[kPfNt];
+            bool grow = !have_ref;
+#pragma unroll
+            for (int n = 0; n < kPfNt; ++n) {
+                tmax[n] = max_across_quads(max3(max3(s[0][n][0], s[0][n][1], s[0][n][2]),
+                                                max3(s[0][n][3], s[1][n][0], s[1][n][1]),
+                                                max3(s[1][n][2], s[1][n][3], -INFINITY)));
+                grow |= tmax[n] > kLazy;
+            }
+            // Rare, wave-uniform: move the reference of the rows whose maximum
+            // exceeds it by more than 2^kLazy (all rows on the first half-tile)
+            // and rescale what they have accumulated.
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {
+#pragma unroll
+                for (int n = 0; n < kPfNt; ++n) {
+                    const float shift = !have_ref || tmax[n] > kLazy ? tmax[n] : 0.0f;
+                    // min(.., 0): on the first half-tile the accumulators are still zero
+                    const float alpha = __builtin_amdgcn_exp2f(fminf(-shift, 0.0f));
+                    nref[n] -= shift;
+                    lsum[n] *= alpha;
+#pragma unroll
+                    for (int kt = 0; kt < 2; ++kt) s[kt][n] -= shift;
 #pragma unroll
                     for (int dt = 0; dt < kDt; ++dt) acc[dt][n] *= alpha;
                 }
+                have_ref = true;
+            }
+            Vec pb[kPfNt];
+#pragma unroll
+            for (int n = 0; n < kPfNt; ++n) {
                 std::uint32_t w[4];
-                float psum = 0.0f;
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt) {
-                    float e[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        e[r] = __builtin_amdgcn_exp2f(s[kt][n][r] - ref);
-                        psum += e[r];
-                    }
-                    w[2 * kt] = M::pack(e[0], e[1]);
-                    w[2 * kt + 1] = M::pack(e[2], e[3]);
+                    w[2 * kt] = M::pack(__builtin_amdgcn_exp2f(s[kt][n][0]), __builtin_amdgcn_exp2f(s[kt][n][1]));
+                    w[2 * kt + 1] = M::pack(__builtin_amdgcn_exp2f(s[kt][n][2]), __builtin_amdgcn_exp2f(s[kt][n][3]));
                 }
-                run_sum[n] += psum;
                 pb[n] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
             }
-            // O^T += V^T P^T for the 32 keys of this half.
+            // O^T += V^T P^T for the 32 keys of this half; l += 1 P^T.
             const auto* vbase = (__attribute__((address_space(3))) char*)(
                 (__attribute__((address_space(3))) std::uint16_t*)vtile);
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
-                const std::uint32_t off = (v_read0 + 32 * h * kRowBytes) ^ (dt << 5);
+                const std::uint32_t off = v_rd[dt] + 32 * h * kRowBytes;
                 const pf_i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off));
                 const pf_i16x4_t hi =
                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off + 16 * kRowBytes));
@@ -306,29 +349,31 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 #pragma unroll
                 for (int n = 0; n < kPfNt; ++n) acc[dt][n] = M::mma(a, pb[n], acc[dt][n]);
             }
+#pragma unroll
+            for (int n = 0; n < kPfNt; ++n) lsum[n] = M::mma(ones, pb[n], lsum[n]);
         }
     };
     Staged set0, set1;
     fetch(0, set0);
     if (ntiles > 1) fetch(1, set1);
     for (std::uint32_t tile = 0; tile < ntiles; tile += 2) {
-        stage(set0);
+        stage(tile, set0);
         __syncthreads();
         if (tile + 2 < ntiles) fetch(tile + 2, set0);
         compute_tile(tile);
         __syncthreads();  // the tile is consumed before the next stage()
         if (tile + 1 >= ntiles) break;
-        stage(set1);
+        stage(tile + 1, set1);
         __syncthreads();
         if (tile + 3 < ntiles) fetch(tile + 3, set1);
         compute_tile(tile + 1);
         __syncthreads();
     }
 
-    // Row sums across the four quads, then O = O^T / l.
+    // O = O^T / l.
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
-        const float l = sum_across_quads(run_sum[n]);
+        const float l = lsum[n][0];
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const int b = wave * kPfNt + n;
         const int g = b % kG;
@@ -385,7 +430,7 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
     const std::uint64_t group = query_heads / num_kv_heads;
     if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128) || !is_pow2(block_size) ||
         block_size > 64 || (group != 1 && group != 2 && group != 4 && group != 8) ||
-        num_blocks >= 0xffffffffULL || num_kv_heads > 65535 || kv_len > 0xffffffffULL ||
+        num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0xffffffffULL ||
         query_heads > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
     }
