@@ -198,30 +198,28 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             st.v[i] = *reinterpret_cast<const uint4*>(vc + off);
         }
     };
-    auto stage = [&](std::uint32_t tile, Staged& st) {
-        // Keys at or past kv_len, or on a missing page, are staged as zeros
-        // (finite V under a zero weight). Uniform test: only the last tile or
-        // a table with gaps takes it.
-        if (table_gaps || (tile + 1) * kPfTile > p.kv_len) {
-#pragma unroll
-            for (int i = 0; i < kChunksPerThread; ++i) {
-                const int row = (tid + kPfThreads * i) / kCpr;
-                const std::uint32_t key = tile * kPfTile + row;
-                const bool zero = key >= p.kv_len || (pages[(tile << tile_pages_shift) + row_page[i]] & kPfMissing);
-                if (zero) {
-                    st.k[i] = make_uint4(0, 0, 0, 0);
-                    st.v[i] = make_uint4(0, 0, 0, 0);
-                }
-            }
-        }
+    auto stage = [&](std::uint32_t tile, const Staged& st) {
         char* kb = reinterpret_cast<char*>(ktile);
         char* vb = reinterpret_cast<char*>(vtile);
+        // Keys at or past kv_len, or on a missing page, are staged as zeros
+        // (finite V under a zero weight). Uniform test: only the last tile or
+        // a table with gaps takes it. The loaded registers are only read
+        // here, never overwritten, so no wait is needed for the other set.
+        const bool fix = table_gaps || (tile + 1) * kPfTile > p.kv_len;
 #pragma unroll
         for (int i = 0; i < kChunksPerThread; ++i) {
             const int id = tid + kPfThreads * i;
             const int row = id / kCpr, c = id % kCpr;
-            *reinterpret_cast<uint4*>(kb + row * kRowBytes + k_slot(row, c) * 16) = st.k[i];
-            *reinterpret_cast<uint4*>(vb + row * kRowBytes + v_slot(row, c) * 16) = st.v[i];
+            uint4 k = st.k[i], v = st.v[i];
+            if (fix) {
+                const std::uint32_t key = tile * kPfTile + row;
+                const std::uint32_t missing_bit = pages[(tile << tile_pages_shift) + row_page[i]] & kPfMissing;
+                const std::uint32_t keep = ((key >= p.kv_len) | (missing_bit != 0)) ? 0u : ~0u;
+                k = make_uint4(k.x & keep, k.y & keep, k.z & keep, k.w & keep);
+                v = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+            }
+            *reinterpret_cast<uint4*>(kb + row * kRowBytes + k_slot(row, c) * 16) = k;
+            *reinterpret_cast<uint4*>(vb + row * kRowBytes + v_slot(row, c) * 16) = v;
         }
     };
     // Transposing V^T reads: lane (q, s) addresses key row 4q + s/4 (+16 for
@@ -353,19 +351,24 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             for (int n = 0; n < kPfNt; ++n) lsum[n] = M::mma(ones, pb[n], lsum[n]);
         }
     };
+    // Every fetch is issued, past the end as a reload of the last tile, so
+    // the loads form one in-order stream and each stage() waits only for the
+    // set it writes (the other set stays in flight).
+    const std::uint32_t last_tile = ntiles - 1;
+    auto clamp_tile = [last_tile](std::uint32_t t) { return t < last_tile ? t : last_tile; };
     Staged set0, set1;
     fetch(0, set0);
-    if (ntiles > 1) fetch(1, set1);
+    fetch(clamp_tile(1), set1);
     for (std::uint32_t tile = 0; tile < ntiles; tile += 2) {
         stage(tile, set0);
         __syncthreads();
-        if (tile + 2 < ntiles) fetch(tile + 2, set0);
+        fetch(clamp_tile(tile + 2), set0);
         compute_tile(tile);
         __syncthreads();  // the tile is consumed before the next stage()
         if (tile + 1 >= ntiles) break;
         stage(tile + 1, set1);
         __syncthreads();
-        if (tile + 3 < ntiles) fetch(tile + 3, set1);
+        fetch(clamp_tile(tile + 3), set1);
         compute_tile(tile + 1);
         __syncthreads();
     }
