@@ -11,6 +11,8 @@
 #include <cstddef>
 #include <cstdint>
 #include <memory>
+#include <utility>
+#include <vector>
 
 namespace kvflux::v2 {
 
@@ -45,6 +47,11 @@ public:
     // Copies the whole K and V page of `source` to the private, unpublished
     // page `destination`, then waits for the copy.
     void copy_block(PhysicalBlockHandle source, PhysicalBlockHandle destination) const;
+    // Batch form (no counterpart in the reference): every (source,
+    // destination) pair in one kernel launch, then one wait. Destinations
+    // must be distinct private, unpublished pages, none of them a source.
+    void copy_blocks(
+        const std::vector<std::pair<PhysicalBlockHandle, PhysicalBlockHandle>>& pairs) const;
 
     // Library-internal: reusable device buffers for per-call metadata.
     detail::DeviceScratch& scratch() const { return *scratch_; }

@@ -12,6 +12,9 @@ namespace kvflux::v2 {
 
 using RequestID = std::uint64_t;
 class PrefixCache;
+namespace detail {
+struct SequenceAccess;  // batched appends of the library (copy_on_write.h, device_batch_table.h)
+}
 
 struct TokenLocation {
     PhysicalBlockID physical_block;
@@ -53,6 +56,7 @@ public:
 
 private:
     friend class PrefixCache;
+    friend struct detail::SequenceAccess;
     void append_cached_full_block(PhysicalBlockHandle handle);
     PhysicalBlockHandle block_handle(std::size_t logical_block) const;
 

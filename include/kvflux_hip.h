@@ -163,6 +163,52 @@ int kvflux_paged_prefill(const void* key_cache, const void* value_cache,
                          void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Callers of the hot path: copy-on-write and device-side batch metadata.
+ *
+ * kvflux_copy_pages: for every pair i of `pairs` (device uint64
+ *   [num_pairs][2] = {source, destination}), the K page and the V page of
+ *   `destination` (page_bytes = num_kv_heads * block_size * head_size * e
+ *   each) become copies of those of `source`, in one launch. Replaces the two
+ *   cudaMemcpyAsync of PagedKVStorage::copy_block
+ *   (reference src/v2/paged_kv_storage.cpp:70-93), called once per shared
+ *   tail page from append_token_cow (src/v2/copy_on_write.cpp:7-16), for a
+ *   whole decode batch. Pairs with an id >= num_blocks or source ==
+ *   destination are skipped. Destinations must be distinct and no
+ *   destination may be a source of the same call (the C++ layer checks).
+ *
+ * kvflux_table_apply: brings a device batch block table (row-major uint64
+ *   [num_rows][table_width], the reference's BatchBlockTable layout,
+ *   include/kvflux/v2/batch_block_table.h:14-22) and its length array
+ *   up to date in place. `updates` is device uint64 [num_updates][4] =
+ *   {row, new_length, block_index, page_id}: seq_lens[row] = new_length and,
+ *   when block_index < table_width, table[row][block_index] = page_id.
+ *   Records of one row must carry the same length and distinct block
+ *   indexes. Replaces the per-call host rebuild and upload of the batch
+ *   table (reference src/v2/batch_block_table.cpp:18-48,
+ *   src/v2/paged_attention.cu:248-313) with O(changed entries) work.
+ *
+ * kvflux_write_paged_kv_tail: kvflux_write_paged_kv for a decode step whose
+ *   slots come from the device batch table: input row r (one token,
+ *   [num_rows][num_kv_heads][head_size]) is written at position
+ *   seq_lens[r] - 1 of table row r, i.e. slot
+ *   table[r][(len - 1) / block_size] * block_size + (len - 1) % block_size
+ *   (reference build_slot_mapping, src/v2/slot_mapping.cpp:8-31, evaluated on
+ *   the device). Rows with a zero length, a block index >= table_width or a
+ *   page id >= num_blocks are skipped.
+ * ------------------------------------------------------------------------- */
+int kvflux_copy_pages(void* key_cache, void* value_cache, uint64_t num_blocks,
+                      uint64_t page_bytes, const uint64_t* pairs, uint64_t num_pairs,
+                      void* stream);
+int kvflux_table_apply(uint64_t* block_table, uint64_t table_width, uint64_t* seq_lens,
+                       uint64_t num_rows, const uint64_t* updates, uint64_t num_updates,
+                       void* stream);
+int kvflux_write_paged_kv_tail(void* key_cache, void* value_cache, uint64_t num_blocks,
+                               uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size,
+                               int dtype, const void* key_new, const void* value_new,
+                               const uint64_t* block_table, uint64_t table_width,
+                               const uint64_t* seq_lens, uint64_t num_rows, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Test and benchmark support (not part of the reference API).
  * kvflux_fill_random writes `count` elements of `dtype` from a counter-based
  * generator: element i depends only on (seed, i), so a CPU checker can

@@ -54,6 +54,10 @@ SIGNATURES = {
                                       _u64, _u64, _u64, _vp, _vp, _vp, _sz, _vp]),
     "kvflux_paged_prefill": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _u64,
                                     _u64, _u64, _vp, _vp, _vp]),
+    "kvflux_copy_pages": (_i32, [_vp, _vp, _u64, _u64, _vp, _u64, _vp]),
+    "kvflux_table_apply": (_i32, [_vp, _u64, _vp, _u64, _vp, _u64, _vp]),
+    "kvflux_write_paged_kv_tail": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _vp, _vp,
+                                          _u64, _vp, _u64, _vp]),
     "kvflux_fill_random": (_i32, [_vp, _u64, _i32, _i32, _u64, _vp]),
     "kvflux_compare_bytes": (_i32, [_vp, _vp, _u64, _pu64]),
 }

@@ -10,6 +10,7 @@
 
 #include "kvflux/v2/batch_block_table.h"
 #include "kvflux/v2/copy_on_write.h"
+#include "kvflux/v2/device_batch_table.h"
 #include "kvflux/v2/prefix_cache.h"
 #include "kvflux/v2/sequence_lifecycle.h"
 #include "kvflux/v2/paged_attention.h"
@@ -212,9 +213,38 @@ PYBIND11_MODULE(_kvflux, m) {
                                 std::size_t head, std::size_t dim) {
             return addr(s.slot_address(k, slot, head, dim));
         })
-        .def("copy_block", &PagedKVStorage::copy_block);
+        .def("copy_block", &PagedKVStorage::copy_block)
+        .def("copy_blocks", [](const PagedKVStorage& s,
+                               const std::vector<std::pair<PhysicalBlockHandle, PhysicalBlockHandle>>& pairs) {
+            py::gil_scoped_release release;
+            s.copy_blocks(pairs);
+        });
 
     m.def("append_token_cow", &append_token_cow);
+    m.def("append_tokens_cow", [](const PagedKVStorage& s, const std::vector<SequenceState*>& seqs) {
+        py::gil_scoped_release release;
+        return append_tokens_cow(s, seqs);
+    });
+
+    py::class_<DeviceBatchTable>(m, "DeviceBatchTable")
+        .def(py::init<const PagedKVStorage&, std::vector<SequenceState*>, std::size_t>(),
+             py::arg("storage"), py::arg("sequences"), py::arg("capacity_blocks"),
+             py::keep_alive<1, 2>(), py::keep_alive<1, 3>())
+        .def("refresh", [](DeviceBatchTable& t) {
+            py::gil_scoped_release release;
+            t.refresh();
+        })
+        .def("rows", &DeviceBatchTable::rows)
+        .def("capacity_blocks", &DeviceBatchTable::capacity_blocks)
+        .def("lengths", &DeviceBatchTable::lengths)
+        .def("device_table", [](const DeviceBatchTable& t) { return addr(t.device_table()); })
+        .def("device_lengths", [](const DeviceBatchTable& t) { return addr(t.device_lengths()); });
+    m.def("decode_step", [](PagedKVStorage& s, DeviceBatchTable& t, std::uintptr_t k, std::uintptr_t v,
+                            std::uintptr_t q, std::uintptr_t o, std::size_t query_heads) {
+        py::gil_scoped_release release;
+        return decode_step(s, t, ptr(k), ptr(v), static_cast<const float*>(ptr(q)),
+                           static_cast<float*>(ptr(o)), query_heads);
+    });
 
     py::class_<SequenceLifecycle>(m, "SequenceLifecycle")
         .def(py::init<RequestID, PhysicalBlockPool&, PagedKVStorage&, std::size_t>(),
@@ -277,5 +307,11 @@ PYBIND11_MODULE(_kvflux, m) {
         py::gil_scoped_release release;
         paged_attention_batch(s, seqs, static_cast<const float*>(ptr(q)),
                               static_cast<float*>(ptr(o)), query_heads);
+    });
+    m.def("paged_attention_batch", [](const PagedKVStorage& s, const DeviceBatchTable& t,
+                                      std::uintptr_t q, std::uintptr_t o, std::size_t query_heads) {
+        py::gil_scoped_release release;
+        paged_attention_batch(s, t, static_cast<const float*>(ptr(q)), static_cast<float*>(ptr(o)),
+                              query_heads);
     });
 }

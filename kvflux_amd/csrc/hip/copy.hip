@@ -1,0 +1,83 @@
+// Batched page copy: copy-on-write of shared pages for many sequences in one
+// launch. The reference copies one page per call with two cudaMemcpyAsync
+// (K page, V page) and a synchronisation (src/v2/paged_kv_storage.cpp:70-93);
+// here every (source, destination) pair of a decode step is one kernel:
+//   K[dst][*] = K[src][*],  V[dst][*] = V[src][*]
+// where a page holds all kv heads contiguously (page_bytes = H * bs * D * e,
+// layout K/V[num_blocks][H][bs][D]). Raw bit copy.
+//
+// gfx950 mapping: grid (pair, 16 KiB part of the page, K or V). A workgroup of
+// 512 threads moves its part with 16-byte loads, all issued before the
+// stores, so one wavefront streams 1 KiB contiguous per instruction. The pair
+// is read once per workgroup (uniform, scalar loads).
+#include "common.h"
+
+namespace kvflux_hip {
+namespace {
+
+constexpr int kCopyThreads = 512;
+constexpr std::uint64_t kPartBytes = 16384;  // bytes of a page per workgroup
+
+template <typename Vec>
+__global__ __launch_bounds__(kCopyThreads) void copy_pages_kernel(char* __restrict__ key_cache,
+                                                                  char* __restrict__ value_cache,
+                                                                  std::uint64_t num_blocks,
+                                                                  std::uint64_t page_bytes,
+                                                                  const std::uint64_t* __restrict__ pairs) {
+    constexpr int kPer = static_cast<int>(kPartBytes / sizeof(Vec) / kCopyThreads);
+    const std::uint64_t src = pairs[2 * static_cast<std::uint64_t>(blockIdx.x)];
+    const std::uint64_t dst = pairs[2 * static_cast<std::uint64_t>(blockIdx.x) + 1];
+    if (src >= num_blocks || dst >= num_blocks || src == dst) return;  // uniform
+    char* base = blockIdx.z == 0 ? key_cache : value_cache;
+    const Vec* from = reinterpret_cast<const Vec*>(base + src * page_bytes);
+    Vec* to = reinterpret_cast<Vec*>(base + dst * page_bytes);
+    const std::uint64_t n = page_bytes / sizeof(Vec);
+    const std::uint64_t first = static_cast<std::uint64_t>(blockIdx.y) * (kPartBytes / sizeof(Vec)) + threadIdx.x;
+    Vec r[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
+        if (i < n) r[u] = from[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
+        if (i < n) to[i] = r[u];
+    }
+}
+
+template <typename Vec>
+int launch_copy(void* kc, void* vc, std::uint64_t num_blocks, std::uint64_t page_bytes,
+                const std::uint64_t* pairs, std::uint64_t num_pairs, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(num_pairs),
+                    static_cast<unsigned>((page_bytes + kPartBytes - 1) / kPartBytes), 2);
+    hipLaunchKernelGGL(copy_pages_kernel<Vec>, grid, dim3(kCopyThreads), 0, s, static_cast<char*>(kc),
+                       static_cast<char*>(vc), num_blocks, page_bytes, pairs);
+    return launch_status("copy_pages_kernel");
+}
+
+} // namespace
+} // namespace kvflux_hip
+
+using namespace kvflux_hip;
+
+extern "C" int kvflux_copy_pages(void* key_cache, void* value_cache, uint64_t num_blocks,
+                                 uint64_t page_bytes, const uint64_t* pairs, uint64_t num_pairs,
+                                 void* stream) {
+    if (num_pairs == 0) return KVFLUX_OK;
+    if (!key_cache || !value_cache || !pairs) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "copy pages: null pointer");
+    if (num_blocks == 0 || page_bytes == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "copy pages: zero dimension");
+    if (num_blocks > (~0ULL) / page_bytes) return fail(KVFLUX_ERR_OVERFLOW, "copy pages: size overflow");
+    if (num_pairs > 0x7fffffffULL || (page_bytes + kPartBytes - 1) / kPartBytes > 65535) {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "copy pages: more than 2^31 pairs or pages above 1 GiB");
+    }
+    const void* ptrs[2] = {key_cache, value_cache};
+    const hipStream_t s = as_stream(stream);
+    switch (copy_width(page_bytes, ptrs, 2)) {
+    case 16: return launch_copy<V16>(key_cache, value_cache, num_blocks, page_bytes, pairs, num_pairs, s);
+    case 8: return launch_copy<V8>(key_cache, value_cache, num_blocks, page_bytes, pairs, num_pairs, s);
+    case 4: return launch_copy<std::uint32_t>(key_cache, value_cache, num_blocks, page_bytes, pairs, num_pairs, s);
+    case 2: return launch_copy<std::uint16_t>(key_cache, value_cache, num_blocks, page_bytes, pairs, num_pairs, s);
+    default: return launch_copy<std::uint8_t>(key_cache, value_cache, num_blocks, page_bytes, pairs, num_pairs, s);
+    }
+}

@@ -21,10 +21,33 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kUnroll = 1;
 
-template <typename Vec>
+// Slot of input row n: from a slot array (write_paged_kv), or the position
+// just appended to sequence n, looked up in a device batch block table
+// (decode append: slot = table[n][(len_n - 1) / bs] * bs + (len_n - 1) % bs).
+// ~0 (never < slot_count) when the row has no valid slot.
+struct SlotList {
+    const std::uint64_t* slots;
+    __device__ std::uint64_t operator()(std::uint64_t n) const { return slots[n]; }
+};
+struct SlotAtTail {
+    const std::uint64_t* table;
+    std::uint64_t width;
+    const std::uint64_t* lens;
+    std::uint64_t block_size, num_blocks;
+    __device__ std::uint64_t operator()(std::uint64_t n) const {
+        const std::uint64_t len = lens[n];
+        if (len == 0) return ~0ULL;
+        const std::uint64_t b = (len - 1) / block_size;
+        if (b >= width) return ~0ULL;
+        const std::uint64_t page = table[n * width + b];
+        return page < num_blocks ? page * block_size + (len - 1) % block_size : ~0ULL;
+    }
+};
+
+template <typename Vec, typename Slots>
 __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel(
     Vec* __restrict__ key_cache, Vec* __restrict__ value_cache, const Vec* __restrict__ key_new,
-    const Vec* __restrict__ value_new, const std::uint64_t* __restrict__ slots,
+    const Vec* __restrict__ value_new, Slots slot_of,
     std::uint32_t total_vectors, FastDiv vectors_per_row, FastDiv heads, FastDiv block_size,
     std::uint32_t slot_count) {
     const std::uint32_t first = blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
@@ -41,7 +64,7 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel(
             const std::uint32_t col = i - row * vectors_per_row.divisor;
             const std::uint32_t token = heads.div(row);
             const std::uint32_t head = row - token * heads.divisor;
-            const std::uint64_t slot = slots[token];
+            const std::uint64_t slot = slot_of(token);
             live[u] = slot < slot_count;  // never write outside the arena
             const std::uint32_t s = static_cast<std::uint32_t>(slot);
             const std::uint32_t page = block_size.div(s);
@@ -63,10 +86,10 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel(
 
 // Same mapping with 64-bit index arithmetic, for arenas or batches whose
 // vector or slot counts do not fit in 32 bits.
-template <typename Vec>
+template <typename Vec, typename Slots>
 __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel_wide(
     Vec* __restrict__ key_cache, Vec* __restrict__ value_cache, const Vec* __restrict__ key_new,
-    const Vec* __restrict__ value_new, const std::uint64_t* __restrict__ slots,
+    const Vec* __restrict__ value_new, Slots slot_of,
     std::uint64_t total_vectors, std::uint64_t vectors_per_row, std::uint64_t heads,
     std::uint64_t block_size, std::uint64_t slot_count) {
     const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
@@ -74,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel_wide(
          i < total_vectors; i += stride) {
         const std::uint64_t row = i / vectors_per_row, col = i % vectors_per_row;
         const std::uint64_t token = row / heads, head = row % heads;
-        const std::uint64_t slot = slots[token];
+        const std::uint64_t slot = slot_of(token);
         if (slot >= slot_count) continue;
         const std::uint64_t d =
             ((slot / block_size * heads + head) * block_size + slot % block_size) *
@@ -84,8 +107,8 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel_wide(
     }
 }
 
-template <typename Vec>
-int launch(void* kc, void* vc, const void* kn, const void* vn, const std::uint64_t* slots,
+template <typename Vec, typename Slots>
+int launch(void* kc, void* vc, const void* kn, const void* vn, Slots slots,
            std::uint64_t tokens, std::uint64_t heads, std::uint64_t block_size,
            std::uint64_t row_bytes, std::uint64_t slot_count, hipStream_t stream) {
     const std::uint64_t vpr = row_bytes / sizeof(Vec);
@@ -96,7 +119,7 @@ int launch(void* kc, void* vc, const void* kn, const void* vn, const std::uint64
         block_size <= limit) {
         const std::uint64_t per_block = kThreads * kUnroll;
         const auto grid = static_cast<unsigned>((total + per_block - 1) / per_block);
-        hipLaunchKernelGGL(paged_kv_write_kernel<Vec>, dim3(grid), dim3(kThreads), 0, stream,
+        hipLaunchKernelGGL((paged_kv_write_kernel<Vec, Slots>), dim3(grid), dim3(kThreads), 0, stream,
                            static_cast<Vec*>(kc), static_cast<Vec*>(vc),
                            static_cast<const Vec*>(kn), static_cast<const Vec*>(vn), slots,
                            static_cast<std::uint32_t>(total),
@@ -107,7 +130,7 @@ int launch(void* kc, void* vc, const void* kn, const void* vn, const std::uint64
     } else {
         const std::uint64_t blocks = (total + kThreads - 1) / kThreads;
         const auto grid = static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
-        hipLaunchKernelGGL(paged_kv_write_kernel_wide<Vec>, dim3(grid), dim3(kThreads), 0, stream,
+        hipLaunchKernelGGL((paged_kv_write_kernel_wide<Vec, Slots>), dim3(grid), dim3(kThreads), 0, stream,
                            static_cast<Vec*>(kc), static_cast<Vec*>(vc),
                            static_cast<const Vec*>(kn), static_cast<const Vec*>(vn), slots, total,
                            vpr, heads, block_size, slot_count);
@@ -120,15 +143,16 @@ int launch(void* kc, void* vc, const void* kn, const void* vn, const std::uint64
 
 using namespace kvflux_hip;
 
-extern "C" int kvflux_write_paged_kv(void* key_cache, void* value_cache, uint64_t num_blocks,
-                                     uint64_t num_kv_heads, uint64_t block_size,
-                                     uint64_t head_size, int dtype, const void* key_new,
-                                     const void* value_new, const uint64_t* slots,
-                                     uint64_t num_tokens, void* stream) {
-    if (num_tokens == 0) return KVFLUX_OK;
+namespace {
+
+// Validation and vector-width dispatch shared by both entry points.
+template <typename Slots>
+int write_rows(void* key_cache, void* value_cache, uint64_t num_blocks, uint64_t num_kv_heads,
+               uint64_t block_size, uint64_t head_size, int dtype, const void* key_new,
+               const void* value_new, Slots slots, uint64_t num_tokens, void* stream) {
     const std::size_t esize = dtype_bytes(dtype);
     if (esize == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
-    if (!key_cache || !value_cache || !key_new || !value_new || !slots) {
+    if (!key_cache || !value_cache || !key_new || !value_new) {
         return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged KV write: null pointer");
     }
     if (num_blocks == 0 || num_kv_heads == 0 || block_size == 0 || head_size == 0) {
@@ -155,4 +179,33 @@ extern "C" int kvflux_write_paged_kv(void* key_cache, void* value_cache, uint64_
                                          slot_count, s);
     default: return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged KV write: misaligned buffers");
     }
+}
+
+} // namespace
+
+extern "C" int kvflux_write_paged_kv(void* key_cache, void* value_cache, uint64_t num_blocks,
+                                     uint64_t num_kv_heads, uint64_t block_size,
+                                     uint64_t head_size, int dtype, const void* key_new,
+                                     const void* value_new, const uint64_t* slots,
+                                     uint64_t num_tokens, void* stream) {
+    if (num_tokens == 0) return KVFLUX_OK;
+    if (!slots) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged KV write: null pointer");
+    return write_rows(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype,
+                      key_new, value_new, SlotList{slots}, num_tokens, stream);
+}
+
+extern "C" int kvflux_write_paged_kv_tail(void* key_cache, void* value_cache, uint64_t num_blocks,
+                                          uint64_t num_kv_heads, uint64_t block_size,
+                                          uint64_t head_size, int dtype, const void* key_new,
+                                          const void* value_new, const uint64_t* block_table,
+                                          uint64_t table_width, const uint64_t* seq_lens,
+                                          uint64_t num_rows, void* stream) {
+    if (num_rows == 0) return KVFLUX_OK;
+    if (!block_table || !seq_lens || table_width == 0) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged KV tail write: null table");
+    }
+    if (num_rows > (~0ULL) / table_width) return fail(KVFLUX_ERR_OVERFLOW, "paged KV tail write: size overflow");
+    return write_rows(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype,
+                      key_new, value_new, SlotAtTail{block_table, table_width, seq_lens, block_size, num_blocks},
+                      num_rows, stream);
 }

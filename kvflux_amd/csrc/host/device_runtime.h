@@ -88,6 +88,7 @@ public:
         return ptr_;
     }
     std::size_t size() const noexcept { return bytes_; }
+    void* data() const noexcept { return ptr_; }
 
 private:
     void* ptr_ = nullptr;
@@ -153,5 +154,38 @@ struct DeviceScratch {
         return out;
     }
 };
+
+inline int abi_dtype(DType dtype) {
+    switch (dtype) {
+    case DType::Float16: return KVFLUX_DTYPE_F16;
+    case DType::BFloat16: return KVFLUX_DTYPE_BF16;
+    case DType::Float32: return KVFLUX_DTYPE_F32;
+    }
+    throw std::invalid_argument("unsupported paged KV dtype");
+}
+
+// Q and O must be device buffers on the storage GPU, disjoint from each
+// other and from the cache.
+inline void validate_q_o(const PagedKVStorage& storage, const float* query, float* output,
+                         std::size_t tensor_bytes) {
+    const auto& layout = storage.layout();
+    require_device_pointer(query, storage.device(), "Q");
+    require_device_pointer(output, storage.device(), "attention output");
+    if (overlaps(query, tensor_bytes, output, tensor_bytes) ||
+        overlaps(query, tensor_bytes, storage.key_base(), layout.total_bytes()) ||
+        overlaps(output, tensor_bytes, storage.key_base(), layout.total_bytes())) {
+        throw std::invalid_argument("Q and attention output must not overlap each other or KV cache");
+    }
+}
+
+// Split-K workspace of an attention call, grown on demand.
+inline void* attention_workspace(const PagedKVStorage& storage, std::size_t rows,
+                                 std::size_t kv_len, std::size_t query_heads, std::size_t* bytes) {
+    const auto& layout = storage.layout();
+    check(kvflux_paged_attention_workspace_size(rows, kv_len, layout.num_kv_heads(), query_heads,
+                                                layout.block_size(), layout.head_size(), bytes),
+          "attention workspace size");
+    return *bytes ? storage.scratch().workspace.reserve(*bytes) : nullptr;
+}
 
 } // namespace kvflux::v2::detail

@@ -18,17 +18,11 @@
 namespace kvflux::v2 {
 namespace {
 
+using detail::abi_dtype;
+using detail::attention_workspace;
 using detail::check;
 using detail::mul_checked;
-
-int abi_dtype(DType dtype) {
-    switch (dtype) {
-    case DType::Float16: return KVFLUX_DTYPE_F16;
-    case DType::BFloat16: return KVFLUX_DTYPE_BF16;
-    case DType::Float32: return KVFLUX_DTYPE_F32;
-    }
-    throw std::invalid_argument("unsupported paged KV dtype");
-}
+using detail::validate_q_o;
 
 // Range and duplicate check in mapping order, so the first offending slot
 // decides the exception exactly as the reference's in-order scan does.
@@ -189,27 +183,6 @@ bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens,
     if (64 % layout.block_size() != 0) return false;
     if (precision == AttentionPrecision::Auto && query_tokens < 16) return false;
     return query_tokens >= 1;
-}
-
-void validate_q_o(const PagedKVStorage& storage, const float* query, float* output,
-                  std::size_t tensor_bytes) {
-    const auto& layout = storage.layout();
-    detail::require_device_pointer(query, storage.device(), "Q");
-    detail::require_device_pointer(output, storage.device(), "attention output");
-    if (detail::overlaps(query, tensor_bytes, output, tensor_bytes) ||
-        detail::overlaps(query, tensor_bytes, storage.key_base(), layout.total_bytes()) ||
-        detail::overlaps(output, tensor_bytes, storage.key_base(), layout.total_bytes())) {
-        throw std::invalid_argument("Q and attention output must not overlap each other or KV cache");
-    }
-}
-
-void* attention_workspace(const PagedKVStorage& storage, std::size_t rows, std::size_t kv_len,
-                          std::size_t query_heads, std::size_t* bytes) {
-    const auto& layout = storage.layout();
-    check(kvflux_paged_attention_workspace_size(rows, kv_len, layout.num_kv_heads(), query_heads,
-                                                layout.block_size(), layout.head_size(), bytes),
-          "attention workspace size");
-    return *bytes ? storage.scratch().workspace.reserve(*bytes) : nullptr;
 }
 
 } // namespace

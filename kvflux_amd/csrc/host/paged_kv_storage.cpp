@@ -6,6 +6,7 @@
 
 #include <limits>
 #include <stdexcept>
+#include <unordered_set>
 
 namespace kvflux::v2 {
 
@@ -70,6 +71,41 @@ void PagedKVStorage::copy_block(PhysicalBlockHandle source, PhysicalBlockHandle 
         detail::check(kvflux_memcpy_async(page_address(KVKind::Value, destination),
                                           page_address(KVKind::Value, source),
                                           layout_.page_bytes(), nullptr), "copy V page");
+        detail::check(kvflux_stream_synchronize(nullptr), "synchronize KV page copy");
+    } catch (...) {
+        (void)kvflux_stream_synchronize(nullptr);
+        throw;
+    }
+}
+
+void PagedKVStorage::copy_blocks(
+    const std::vector<std::pair<PhysicalBlockHandle, PhysicalBlockHandle>>& pairs) const {
+    if (pairs.empty()) return;
+    std::vector<std::uint64_t> ids;
+    ids.reserve(2 * pairs.size());
+    std::unordered_set<PhysicalBlockID> destinations;
+    for (const auto& [source, destination] : pairs) {
+        const auto from = pool_.id(source);
+        const auto to = pool_.id(destination);
+        if (from == to || pool_.ref_count(destination) != 1 || pool_.is_published(destination) ||
+            !destinations.insert(to).second) {
+            throw std::invalid_argument("copy destination must be a private, unpublished page");
+        }
+        ids.push_back(from);
+        ids.push_back(to);
+    }
+    for (std::size_t i = 0; i < ids.size(); i += 2) {
+        if (destinations.count(ids[i])) {
+            throw std::invalid_argument("a copy source is also a destination of the batch");
+        }
+    }
+    detail::DeviceGuard guard(device_);
+    const auto dev = scratch_->upload({{ids.data(), ids.size() * sizeof(std::uint64_t)}});
+    try {
+        // All pages must land before the callers switch their table entries.
+        detail::check(kvflux_copy_pages(key_base(), value_base(), layout_.num_blocks(),
+                                        layout_.page_bytes(), dev[0], pairs.size(), nullptr),
+                      "copy KV pages");
         detail::check(kvflux_stream_synchronize(nullptr), "synchronize KV page copy");
     } catch (...) {
         (void)kvflux_stream_synchronize(nullptr);
