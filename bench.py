@@ -17,6 +17,9 @@ Also measured in the same run (sub-objects of the JSON line):
   prefill: causal paged prefill on MFMA, 8 sequences x 4096 tokens written
            through slot_mapping into random pages, 32 q / 8 kv heads, D=128,
            BF16; TFLOP/s and MFMA utilisation against 2.5 PFLOP/s dense BF16
+  cow    : batched copy-on-write page copy, 4096 pairs of 32 KiB K and V pages
+  decode_step: whole decode steps on the decode batch through the C++ API
+           (device batch table) against the reference API's composition
   cpu_baseline : the CPU oracle (gather + double-precision attention, one
            thread) on a bounded sample of the decode rows, timed here.
 
@@ -166,8 +169,10 @@ def bench_decode(v2, args, stream):
         cpu_s += time.perf_counter() - t0
         cpu_bytes += L * kv_token_bytes
         err = max(err, float(np.abs(ref - out[r * Hq * D:(r + 1) * Hq * D]).max()))
+    step = None if args.skip_aux else bench_decode_step(v2, args, storage, seqs, width, ms)
     del seqs, base
     return {
+        "decode_step": step,
         "ms": ms,
         "unique_bytes": unique_bytes,
         "logical_bytes": logical_bytes,
@@ -180,6 +185,92 @@ def bench_decode(v2, args, stream):
                 "sample": f"{len(sample_rows)} decode rows (L={[int(lens[r]) for r in sample_rows]}, "
                           "32 q heads each): page gather + double-precision softmax attention, 1 thread"},
     }
+
+
+def bench_decode_step(v2, args, storage, seqs, width, kernel_ms):
+    """Whole decode steps on the same batch through the C++ API (synchronous):
+    decode_step (device table, batched copy-on-write, tail-slot write, batch
+    attention, one sync) against the reference API's composition of the same
+    step (append_token_cow per row, slot mapping + write_paged_kv, host batch
+    table + paged_attention_batch). Both include host work and every sync."""
+    from kvflux_amd import capi, device
+
+    B, H, Hq, D = len(seqs), 8, 32, 128
+    kn, vn = device.DeviceBuffer(B * H * D * 2), device.DeviceBuffer(B * H * D * 2)
+    device.fill_random(kn.ptr, B * H * D, capi.DTYPE_BF16, 1, args.seed + 5)
+    device.fill_random(vn.ptr, B * H * D, capi.DTYPE_BF16, 1, args.seed + 6)
+    q, o = device.DeviceBuffer(B * Hq * D * 4), device.DeviceBuffer(B * Hq * D * 4)
+    device.fill_random(q.ptr, B * Hq * D, capi.DTYPE_F32, 1, args.seed + 7)
+    table = v2.DeviceBatchTable(storage, seqs, width + 64)
+    steps = 10
+
+    def run_device(n):
+        t0 = time.perf_counter()
+        for _ in range(n):
+            v2.decode_step(storage, table, kn.ptr, vn.ptr, q.ptr, o.ptr, Hq)
+        return (time.perf_counter() - t0) / n * 1e3
+
+    def run_composed(n):
+        t0 = time.perf_counter()
+        for _ in range(n):
+            for s in seqs:
+                v2.append_token_cow(storage, s)
+            v2.write_paged_kv(storage, kn.ptr, vn.ptr,
+                              v2.build_slot_mapping([(s, s.num_tokens() - 1) for s in seqs]))
+            v2.paged_attention_batch(storage, seqs, q.ptr, o.ptr, Hq)
+        return (time.perf_counter() - t0) / n * 1e3
+
+    run_device(2)
+    dev_ms = run_device(steps)
+    run_composed(2)
+    comp_ms = run_composed(steps)
+    max_blocks = max(s.num_allocated_blocks() for s in seqs)
+    return {
+        "rows": B,
+        "ms": dev_ms,
+        "composed_reference_api_ms": comp_ms,
+        "attention_kernel_ms": kernel_ms,
+        "host_to_device_bytes_per_step": B * 32,
+        "composed_host_to_device_bytes_per_step": B * 8 + B * max_blocks * 8 + B * 8,
+        "note": "synchronous C++ API, host work included; steps append one token per row",
+    }
+
+
+# --------------------------------------------------------------------- copy-on-write
+def bench_cow(v2, args, stream):
+    """Batched page copy (copy-on-write) kernel: 4096 (source, destination)
+    pairs of 32 KiB pages (8 kv heads x 16 tokens x 128, BF16) in a
+    65536-page pool; K and V pages both copied."""
+    from kvflux_amd import capi, device
+
+    P, H, D, bs = 4096, 8, 128, 16
+    rng = np.random.default_rng(args.seed + 40)
+    pool = v2.PhysicalBlockPool(65536, bs)
+    storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
+    n = storage.layout().cache_bytes() // 2
+    device.fill_random(storage.key_base(), n, capi.DTYPE_BF16, 1, args.seed + 41)
+    device.fill_random(storage.value_base(), n, capi.DTYPE_BF16, 1, args.seed + 42)
+    order = rng.permutation(65536)
+    src, dst = order[:P], order[P:2 * P]
+    pairs = np.stack([src, dst], 1).astype(np.uint64).reshape(-1)
+    pd = device.to_device(pairs)
+    lib = capi.lib()
+    kb, vb = storage.key_base(), storage.value_base()
+    page_bytes = storage.layout().page_bytes()
+
+    def launch():
+        capi.check(lib.kvflux_copy_pages(kb, vb, 65536, page_bytes, pd.ptr, P, stream))
+
+    ms = time_launches(launch, stream, args.warmup, max(args.steps, 50))
+    mism = 0
+    for i in range(0, P, P // 64):  # sampled pairs, bit-exact
+        for base in (kb, vb):
+            a = device.memcpy_d2h(base + int(src[i]) * page_bytes, page_bytes, np.uint8)
+            b = device.memcpy_d2h(base + int(dst[i]) * page_bytes, page_bytes, np.uint8)
+            mism += int((a != b).sum())
+    bytes_step = 2 * 2 * P * page_bytes
+    return {"kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9, "bytes": bytes_step,
+            "pairs": P, "page_bytes": page_bytes, "pairs_checked": 64, "mismatched_bytes": mism}
 
 
 # --------------------------------------------------------------------- write
@@ -450,7 +541,11 @@ def main() -> int:
         log("prefill ...")
         aux["prefill"] = bench_prefill(v2, args, stream.handle)
         log(f"prefill {aux['prefill']}")
-        for key in ("write", "gather_BFloat16", "gather_Float16"):
+        log("copy-on-write ...")
+        aux["cow"] = bench_cow(v2, args, stream.handle)
+        log(f"cow {aux['cow']}")
+        aux["decode_step"] = dec["decode_step"]
+        for key in ("write", "gather_BFloat16", "gather_Float16", "cow"):
             aux[key]["pct_of_peak"] = round(100 * aux[key]["GBps"] / PEAK_HBM_GBPS, 2)
 
     s = dec["ms"] * 1e-3
