@@ -58,8 +58,12 @@ int kvflux_get_device(int* device);
 int kvflux_set_device(int device);
 int kvflux_device_malloc(void** ptr, size_t bytes);   /* on the current device */
 int kvflux_device_free(void* ptr);
+/* Page-locked host memory, mapped into the device address space. */
 int kvflux_host_malloc_pinned(void** ptr, size_t bytes);
 int kvflux_host_free_pinned(void* ptr);
+/* Device-side address of a pointer returned by kvflux_host_malloc_pinned
+ * (what kernels must be given to read or write that host memory). */
+int kvflux_host_device_pointer(void* host_ptr, void** device_ptr);
 /* *device = owning device id if `ptr` is device memory, else -1 (never fails
  * for host pointers; clears any sticky runtime error it provokes). */
 int kvflux_pointer_device(const void* ptr, int* device);
@@ -77,6 +81,11 @@ int kvflux_event_create(void** event);
 int kvflux_event_destroy(void* event);
 int kvflux_event_record(void* event, void* stream);
 int kvflux_event_elapsed_ms(float* ms, void* start, void* stop);
+int kvflux_event_synchronize(void* event);
+/* *complete = 1 when all work before the event has finished, else 0. */
+int kvflux_event_query(void* event, int* complete);
+/* Work enqueued on `stream` after this call waits for `event`. */
+int kvflux_stream_wait_event(void* stream, void* event);
 
 /* ---------------------------------------------------------------------------
  * Hot path 1: paged KV write (scatter by slot).
@@ -207,6 +216,26 @@ int kvflux_write_paged_kv_tail(void* key_cache, void* value_cache, uint64_t num_
                                int dtype, const void* key_new, const void* value_new,
                                const uint64_t* block_table, uint64_t table_width,
                                const uint64_t* seq_lens, uint64_t num_rows, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * GPU <-> CPU chunk transfer (KV offload).
+ *
+ * kvflux_copy_chunks: for every pair i of `pairs` (device uint64
+ *   [num_pairs][2] = {source address, destination address}), copies
+ *   chunk_bytes bytes, all pairs in one launch. Either side may be device
+ *   memory of the current device or pinned host memory from
+ *   kvflux_host_malloc_pinned (mapped into the device address space), so one
+ *   launch offloads (device -> host), onloads (host -> device) or moves a
+ *   whole batch of chunks whose host slots are scattered. Every address must
+ *   be aligned to the largest power of two (at most 16) dividing
+ *   chunk_bytes; ranges must not overlap. Replaces one cudaMemcpyAsync per
+ *   chunk of GpuCpuTransfer::begin_offload / begin_onload
+ *   (reference src/v3/gpu_cpu_transfer.cpp:32-95) for a batch of chunks.
+ *   Host addresses (in `pairs`, and `pairs` itself when it is host memory)
+ *   are the device-side ones from kvflux_host_device_pointer.
+ * ------------------------------------------------------------------------- */
+int kvflux_copy_chunks(const uint64_t* pairs, uint64_t num_pairs, uint64_t chunk_bytes,
+                       void* stream);
 
 /* ---------------------------------------------------------------------------
  * Test and benchmark support (not part of the reference API).

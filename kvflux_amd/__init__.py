@@ -1,7 +1,8 @@
 """MI355X (gfx950) paged-KV data path with the kvflux::v2 API.
 
 `kvflux_amd.v2` is the Python binding of the C++17 layer (same class and
-function names as kvflux::v2); `kvflux_amd.capi` is the raw C ABI of
+function names as kvflux::v2), `kvflux_amd.v3` that of the tiered cache
+(kvflux::v3); `kvflux_amd.capi` is the raw C ABI of
 libkvflux_hip.so; `kvflux_amd.device` holds device buffers, streams and
 events made through that ABI. Nothing here falls back to a CPU path: if the
 native libraries are missing, importing `v2` raises.
@@ -22,5 +23,9 @@ def __getattr__(name):
     if name == "v2":
         mod = _load_v2()
         globals()["v2"] = mod
+        return mod
+    if name == "v3":  # tiered cache (GPU <-> CPU chunk transfer), kvflux::v3
+        mod = _load_v2().v3
+        globals()["v3"] = mod
         return mod
     raise AttributeError(name)

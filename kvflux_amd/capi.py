@@ -32,6 +32,7 @@ SIGNATURES = {
     "kvflux_device_free": (_i32, [_vp]),
     "kvflux_host_malloc_pinned": (_i32, [C.POINTER(_vp), _sz]),
     "kvflux_host_free_pinned": (_i32, [_vp]),
+    "kvflux_host_device_pointer": (_i32, [_vp, C.POINTER(_vp)]),
     "kvflux_pointer_device": (_i32, [_vp, C.POINTER(C.c_int)]),
     "kvflux_memcpy_async": (_i32, [_vp, _vp, _sz, _vp]),
     "kvflux_memcpy": (_i32, [_vp, _vp, _sz]),
@@ -44,6 +45,9 @@ SIGNATURES = {
     "kvflux_event_destroy": (_i32, [_vp]),
     "kvflux_event_record": (_i32, [_vp, _vp]),
     "kvflux_event_elapsed_ms": (_i32, [C.POINTER(C.c_float), _vp, _vp]),
+    "kvflux_event_synchronize": (_i32, [_vp]),
+    "kvflux_event_query": (_i32, [_vp, C.POINTER(C.c_int)]),
+    "kvflux_stream_wait_event": (_i32, [_vp, _vp]),
     "kvflux_write_paged_kv": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _vp, _vp,
                                      _u64, _vp]),
     "kvflux_gather_paged_kv": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _vp,
@@ -58,6 +62,7 @@ SIGNATURES = {
     "kvflux_table_apply": (_i32, [_vp, _u64, _vp, _u64, _vp, _u64, _vp]),
     "kvflux_write_paged_kv_tail": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _vp, _vp,
                                           _u64, _vp, _u64, _vp]),
+    "kvflux_copy_chunks": (_i32, [_vp, _u64, _u64, _vp]),
     "kvflux_fill_random": (_i32, [_vp, _u64, _i32, _i32, _u64, _vp]),
     "kvflux_compare_bytes": (_i32, [_vp, _vp, _u64, _pu64]),
 }

@@ -17,6 +17,10 @@
 #include "kvflux/v2/paged_kv_read.h"
 #include "kvflux/v2/paged_kv_write.h"
 #include "kvflux/v2/reference_attention.h"
+#include "kvflux/v3/cache_directory.h"
+#include "kvflux/v3/gpu_chunk_store.h"
+#include "kvflux/v3/gpu_cpu_transfer.h"
+#include "kvflux/v3/pinned_chunk_pool.h"
 
 #include <cstdint>
 #include <stdexcept>
@@ -38,6 +42,109 @@ void* ptr(std::uintptr_t address) { return reinterpret_cast<void*>(address); }
 std::uintptr_t addr(const void* p) { return reinterpret_cast<std::uintptr_t>(p); }
 
 } // namespace
+
+static void bind_v3(py::module_ v3m) {
+    namespace v3 = kvflux::v3;
+    py::enum_<v3::StorageTier>(v3m, "StorageTier")
+        .value("GPU", v3::StorageTier::GPU)
+        .value("CPU", v3::StorageTier::CPU)
+        .value("NVME", v3::StorageTier::NVME);
+    py::enum_<v3::ChunkState>(v3m, "ChunkState")
+        .value("READY", v3::ChunkState::READY)
+        .value("COPYING", v3::ChunkState::COPYING)
+        .value("LOADING", v3::ChunkState::LOADING)
+        .value("EVICTING", v3::ChunkState::EVICTING)
+        .value("ERROR", v3::ChunkState::ERROR);
+    py::class_<v3::TierLocation>(v3m, "TierLocation")
+        .def(py::init([](std::size_t slot, std::uint64_t generation) { return v3::TierLocation{slot, generation}; }),
+             py::arg("slot"), py::arg("generation"))
+        .def_readonly("slot", &v3::TierLocation::slot)
+        .def_readonly("generation", &v3::TierLocation::generation)
+        .def("__eq__", &v3::TierLocation::operator==);
+    py::class_<v3::Tier>(v3m, "Tier")
+        .def("kind", &v3::Tier::kind)
+        .def("chunk_bytes", &v3::Tier::chunk_bytes)
+        .def("capacity", &v3::Tier::capacity)
+        .def("allocated_chunks", &v3::Tier::allocated_chunks)
+        .def("available", &v3::Tier::available)
+        .def("used_bytes", &v3::Tier::used_bytes)
+        .def("available_bytes", &v3::Tier::available_bytes)
+        .def("allocate", &v3::Tier::allocate)
+        .def("release", &v3::Tier::release);
+    py::class_<v3::SlotTier, v3::Tier>(v3m, "SlotTier");
+    py::class_<v3::CpuTier, v3::SlotTier>(v3m, "CpuTier").def(py::init<std::size_t, std::size_t>());
+    py::class_<v3::NvmeTier, v3::SlotTier>(v3m, "NvmeTier").def(py::init<std::size_t, std::size_t>());
+    py::class_<v3::GpuTier, v3::Tier>(v3m, "GpuTier")
+        .def(py::init<PhysicalBlockPool&, std::size_t>(), py::keep_alive<1, 2>());
+    py::class_<v3::CacheKey>(v3m, "CacheKey")
+        .def_readonly("model_id", &v3::CacheKey::model_id)
+        .def_readonly("prefix_hash", &v3::CacheKey::prefix_hash)
+        .def_readonly("prefix", &v3::CacheKey::prefix)
+        .def("__eq__", &v3::CacheKey::operator==);
+    v3m.def("make_cache_key", &v3::make_cache_key);
+    py::class_<v3::Replica>(v3m, "Replica")
+        .def_readonly("location", &v3::Replica::location)
+        .def_readonly("state", &v3::Replica::state);
+    py::class_<v3::ChunkRecord>(v3m, "ChunkRecord")
+        .def_readonly("version", &v3::ChunkRecord::version)
+        .def_readonly("ref_count", &v3::ChunkRecord::ref_count)
+        .def_readonly("pin_count", &v3::ChunkRecord::pin_count)
+        .def_readonly("gpu", &v3::ChunkRecord::gpu)
+        .def_readonly("cpu", &v3::ChunkRecord::cpu)
+        .def_readonly("nvme", &v3::ChunkRecord::nvme);
+    py::class_<v3::CacheDirectory>(v3m, "CacheDirectory")
+        .def(py::init<v3::Tier&, v3::Tier&, v3::Tier&>(), py::keep_alive<1, 2>(), py::keep_alive<1, 3>(),
+             py::keep_alive<1, 4>())
+        .def("create", &v3::CacheDirectory::create)
+        .def("contains", &v3::CacheDirectory::contains)
+        .def("at", &v3::CacheDirectory::at, py::return_value_policy::copy)
+        .def("size", &v3::CacheDirectory::size)
+        .def("place", &v3::CacheDirectory::place, py::arg("key"), py::arg("tier"),
+             py::arg("state") = v3::ChunkState::READY)
+        .def("remove", &v3::CacheDirectory::remove)
+        .def("set_state", &v3::CacheDirectory::set_state)
+        .def("pin", &v3::CacheDirectory::pin)
+        .def("unpin", &v3::CacheDirectory::unpin)
+        .def("destroy", &v3::CacheDirectory::destroy)
+        .def("replica_count", &v3::CacheDirectory::replica_count);
+    py::class_<v3::HostChunkBuffers>(v3m, "HostChunkBuffers")
+        .def("chunk_bytes", &v3::HostChunkBuffers::chunk_bytes)
+        .def("slots", &v3::HostChunkBuffers::slots)
+        .def("data", [](v3::HostChunkBuffers& b, std::size_t slot) { return addr(b.data(slot)); });
+    py::class_<v3::HeapChunkPool, v3::HostChunkBuffers>(v3m, "HeapChunkPool")
+        .def(py::init<std::size_t, std::size_t>());
+    py::class_<v3::PinnedChunkPool, v3::HostChunkBuffers>(v3m, "PinnedChunkPool")
+        .def(py::init<std::size_t, std::size_t>())
+        .def("device_data", [](const v3::PinnedChunkPool& b, std::size_t slot) { return addr(b.device_data(slot)); });
+    py::class_<v3::GpuChunkStore>(v3m, "GpuChunkStore")
+        .def(py::init<std::size_t, std::size_t, int>(), py::arg("total_slots"), py::arg("chunk_bytes"),
+             py::arg("device") = 0)
+        .def("device_ptr", [](const v3::GpuChunkStore& g, const v3::TierLocation& l) { return addr(g.device_ptr(l)); })
+        .def("chunk_bytes", &v3::GpuChunkStore::chunk_bytes)
+        .def("slots", &v3::GpuChunkStore::slots);
+    py::class_<v3::GpuCpuTransfer>(v3m, "GpuCpuTransfer")
+        .def(py::init<v3::CacheDirectory&, v3::GpuChunkStore&, v3::HostChunkBuffers&, int>(), py::arg("directory"),
+             py::arg("gpu_store"), py::arg("cpu_buffers"), py::arg("device") = 0, py::keep_alive<1, 2>(),
+             py::keep_alive<1, 3>(), py::keep_alive<1, 4>())
+        .def("begin_offload", [](v3::GpuCpuTransfer& t, const v3::CacheKey& k) { t.begin_offload(k); })
+        .def("begin_onload", [](v3::GpuCpuTransfer& t, const v3::CacheKey& k) { t.begin_onload(k); })
+        .def("begin_offload_batch", [](v3::GpuCpuTransfer& t, const std::vector<v3::CacheKey>& k) {
+            t.begin_offload(k);
+        })
+        .def("begin_onload_batch", [](v3::GpuCpuTransfer& t, const std::vector<v3::CacheKey>& k) {
+            t.begin_onload(k);
+        })
+        .def("finish_offload", [](v3::GpuCpuTransfer& t, const v3::CacheKey& k, bool release) {
+            py::gil_scoped_release unlock;
+            t.finish_offload(k, release);
+        })
+        .def("finish_onload", [](v3::GpuCpuTransfer& t, const v3::CacheKey& k, bool release) {
+            py::gil_scoped_release unlock;
+            t.finish_onload(k, release);
+        })
+        .def("has_pending", &v3::GpuCpuTransfer::has_pending)
+        .def("stream", [](const v3::GpuCpuTransfer& t) { return addr(t.stream()); });
+}
 
 PYBIND11_MODULE(_kvflux, m) {
     m.doc() = "kvflux::v2 paged-KV data path (MI355X / gfx950)";
@@ -308,6 +415,7 @@ PYBIND11_MODULE(_kvflux, m) {
         paged_attention_batch(s, seqs, static_cast<const float*>(ptr(q)),
                               static_cast<float*>(ptr(o)), query_heads);
     });
+    bind_v3(m.def_submodule("v3", "kvflux::v3 tiered cache: tiers, directory, GPU <-> CPU transfer"));
     m.def("paged_attention_batch", [](const PagedKVStorage& s, const DeviceBatchTable& t,
                                       std::uintptr_t q, std::uintptr_t o, std::size_t query_heads) {
         py::gil_scoped_release release;

@@ -10,6 +10,12 @@
 // 512 threads moves its part with 16-byte loads, all issued before the
 // stores, so one wavefront streams 1 KiB contiguous per instruction. The pair
 // is read once per workgroup (uniform, scalar loads).
+//
+// The same part copy moves KV chunks between the GPU and pinned host memory
+// (offload / onload): kvflux_copy_chunks takes (source, destination) address
+// pairs, so a batch of chunks whose host slots are scattered is one launch
+// instead of one cudaMemcpyAsync per chunk (reference
+// src/v3/gpu_cpu_transfer.cpp:32-95).
 #include "common.h"
 
 namespace kvflux_hip {
@@ -18,20 +24,10 @@ namespace {
 constexpr int kCopyThreads = 512;
 constexpr std::uint64_t kPartBytes = 16384;  // bytes of a page per workgroup
 
+// Part blockIdx.y of an n-vector range: every load issued before the stores.
 template <typename Vec>
-__global__ __launch_bounds__(kCopyThreads) void copy_pages_kernel(char* __restrict__ key_cache,
-                                                                  char* __restrict__ value_cache,
-                                                                  std::uint64_t num_blocks,
-                                                                  std::uint64_t page_bytes,
-                                                                  const std::uint64_t* __restrict__ pairs) {
+__device__ inline void copy_part(const Vec* __restrict__ from, Vec* __restrict__ to, std::uint64_t n) {
     constexpr int kPer = static_cast<int>(kPartBytes / sizeof(Vec) / kCopyThreads);
-    const std::uint64_t src = pairs[2 * static_cast<std::uint64_t>(blockIdx.x)];
-    const std::uint64_t dst = pairs[2 * static_cast<std::uint64_t>(blockIdx.x) + 1];
-    if (src >= num_blocks || dst >= num_blocks || src == dst) return;  // uniform
-    char* base = blockIdx.z == 0 ? key_cache : value_cache;
-    const Vec* from = reinterpret_cast<const Vec*>(base + src * page_bytes);
-    Vec* to = reinterpret_cast<Vec*>(base + dst * page_bytes);
-    const std::uint64_t n = page_bytes / sizeof(Vec);
     const std::uint64_t first = static_cast<std::uint64_t>(blockIdx.y) * (kPartBytes / sizeof(Vec)) + threadIdx.x;
     Vec r[kPer];
 #pragma unroll
@@ -47,6 +43,20 @@ __global__ __launch_bounds__(kCopyThreads) void copy_pages_kernel(char* __restri
 }
 
 template <typename Vec>
+__global__ __launch_bounds__(kCopyThreads) void copy_pages_kernel(char* __restrict__ key_cache,
+                                                                  char* __restrict__ value_cache,
+                                                                  std::uint64_t num_blocks,
+                                                                  std::uint64_t page_bytes,
+                                                                  const std::uint64_t* __restrict__ pairs) {
+    const std::uint64_t src = pairs[2 * static_cast<std::uint64_t>(blockIdx.x)];
+    const std::uint64_t dst = pairs[2 * static_cast<std::uint64_t>(blockIdx.x) + 1];
+    if (src >= num_blocks || dst >= num_blocks || src == dst) return;  // uniform
+    char* base = blockIdx.z == 0 ? key_cache : value_cache;
+    copy_part(reinterpret_cast<const Vec*>(base + src * page_bytes), reinterpret_cast<Vec*>(base + dst * page_bytes),
+              page_bytes / sizeof(Vec));
+}
+
+template <typename Vec>
 int launch_copy(void* kc, void* vc, std::uint64_t num_blocks, std::uint64_t page_bytes,
                 const std::uint64_t* pairs, std::uint64_t num_pairs, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(num_pairs),
@@ -56,10 +66,44 @@ int launch_copy(void* kc, void* vc, std::uint64_t num_blocks, std::uint64_t page
     return launch_status("copy_pages_kernel");
 }
 
+// Batched chunk copy between arbitrary device-visible addresses (device
+// memory, or pinned host memory mapped into the device address space):
+// grid (pair, 16 KiB part).
+template <typename Vec>
+__global__ __launch_bounds__(kCopyThreads) void copy_chunks_kernel(const std::uint64_t* __restrict__ pairs,
+                                                                   std::uint64_t chunk_bytes) {
+    copy_part(reinterpret_cast<const Vec*>(pairs[2 * static_cast<std::uint64_t>(blockIdx.x)]),
+              reinterpret_cast<Vec*>(pairs[2 * static_cast<std::uint64_t>(blockIdx.x) + 1]), chunk_bytes / sizeof(Vec));
+}
+
+template <typename Vec>
+int launch_chunks(const std::uint64_t* pairs, std::uint64_t num_pairs, std::uint64_t chunk_bytes, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(num_pairs),
+                    static_cast<unsigned>((chunk_bytes + kPartBytes - 1) / kPartBytes));
+    hipLaunchKernelGGL(copy_chunks_kernel<Vec>, grid, dim3(kCopyThreads), 0, s, pairs, chunk_bytes);
+    return launch_status("copy_chunks_kernel");
+}
+
 } // namespace
 } // namespace kvflux_hip
 
 using namespace kvflux_hip;
+
+extern "C" int kvflux_copy_chunks(const uint64_t* pairs, uint64_t num_pairs, uint64_t chunk_bytes, void* stream) {
+    if (num_pairs == 0 || chunk_bytes == 0) return KVFLUX_OK;
+    if (!pairs) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "copy chunks: null pointer");
+    if (num_pairs > 0x7fffffffULL || (chunk_bytes + kPartBytes - 1) / kPartBytes > 65535) {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "copy chunks: more than 2^31 pairs or chunks above 1 GiB");
+    }
+    const hipStream_t s = as_stream(stream);
+    switch (copy_width(chunk_bytes, nullptr, 0)) {
+    case 16: return launch_chunks<V16>(pairs, num_pairs, chunk_bytes, s);
+    case 8: return launch_chunks<V8>(pairs, num_pairs, chunk_bytes, s);
+    case 4: return launch_chunks<std::uint32_t>(pairs, num_pairs, chunk_bytes, s);
+    case 2: return launch_chunks<std::uint16_t>(pairs, num_pairs, chunk_bytes, s);
+    default: return launch_chunks<std::uint8_t>(pairs, num_pairs, chunk_bytes, s);
+    }
+}
 
 extern "C" int kvflux_copy_pages(void* key_cache, void* value_cache, uint64_t num_blocks,
                                  uint64_t page_bytes, const uint64_t* pairs, uint64_t num_pairs,

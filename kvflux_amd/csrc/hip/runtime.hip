@@ -192,10 +192,16 @@ int kvflux_device_free(void* ptr) { return hip_status(hipFree(ptr), "hipFree"); 
 int kvflux_host_malloc_pinned(void** ptr, size_t bytes) {
     if (!ptr) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "ptr is null");
     *ptr = nullptr;
-    return hip_status(hipHostMalloc(ptr, bytes, hipHostMallocDefault), "hipHostMalloc");
+    return hip_status(hipHostMalloc(ptr, bytes, hipHostMallocMapped), "hipHostMalloc");
 }
 
 int kvflux_host_free_pinned(void* ptr) { return hip_status(hipHostFree(ptr), "hipHostFree"); }
+
+int kvflux_host_device_pointer(void* host_ptr, void** device_ptr) {
+    if (!host_ptr || !device_ptr) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "pointer is null");
+    *device_ptr = nullptr;
+    return hip_status(hipHostGetDevicePointer(device_ptr, host_ptr, 0), "hipHostGetDevicePointer");
+}
 
 int kvflux_pointer_device(const void* ptr, int* device) {
     if (!device) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "device is null");
@@ -272,6 +278,22 @@ int kvflux_event_destroy(void* event) {
 int kvflux_event_record(void* event, void* stream) {
     return hip_status(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)),
                       "hipEventRecord");
+}
+
+int kvflux_event_synchronize(void* event) {
+    return hip_status(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+}
+
+int kvflux_event_query(void* event, int* complete) {
+    if (!complete) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "complete is null");
+    const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(event));
+    *complete = e == hipSuccess;
+    return e == hipErrorNotReady ? KVFLUX_OK : hip_status(e, "hipEventQuery");
+}
+
+int kvflux_stream_wait_event(void* stream, void* event) {
+    return hip_status(hipStreamWaitEvent(as_stream(stream), static_cast<hipEvent_t>(event), 0),
+                      "hipStreamWaitEvent");
 }
 
 int kvflux_event_elapsed_ms(float* ms, void* start, void* stop) {
