@@ -20,6 +20,8 @@ Also measured in the same run (sub-objects of the JSON line):
   cow    : batched copy-on-write page copy, 4096 pairs of 32 KiB K and V pages
   decode_step: whole decode steps on the decode batch through the C++ API
            (device batch table) against the reference API's composition
+  offload: GPU <-> CPU chunk transfer (tiered cache), per-chunk DMA against
+           one kernel per batch, and overlap with the decode kernel
   cpu_baseline : the CPU oracle (gather + double-precision attention, one
            thread) on a bounded sample of the decode rows, timed here.
 
@@ -170,9 +172,11 @@ def bench_decode(v2, args, stream):
         cpu_bytes += L * kv_token_bytes
         err = max(err, float(np.abs(ref - out[r * Hq * D:(r + 1) * Hq * D]).max()))
     step = None if args.skip_aux else bench_decode_step(v2, args, storage, seqs, width, ms)
+    offload = None if args.skip_aux else bench_offload(v2, args, launch, stream, ms)
     del seqs, base
     return {
         "decode_step": step,
+        "offload": offload,
         "ms": ms,
         "unique_bytes": unique_bytes,
         "logical_bytes": logical_bytes,
@@ -234,6 +238,87 @@ def bench_decode_step(v2, args, storage, seqs, width, kernel_ms):
         "composed_host_to_device_bytes_per_step": B * 8 + B * max_blocks * 8 + B * 8,
         "note": "synchronous C++ API, host work included; steps append one token per row",
     }
+
+
+# --------------------------------------------------------------------- offload
+def bench_offload(v2, args, decode_launch, stream, decode_ms):
+    """GPU <-> CPU chunk transfer of the tiered cache (kvflux::v3): 4096 chunks
+    of 64 KiB (256 MiB) with scattered pinned host slots, moved
+    * one DMA copy per chunk (the reference's GpuCpuTransfer, one
+      cudaMemcpyAsync per begin_offload / begin_onload), and
+    * one kernel per batch (begin_offload_batch / begin_onload_batch).
+    Rates are bytes over the transfer stream's own event time. Each offload
+    is repeated while decode steps run on the compute stream, to see how
+    much the two slow each other."""
+    import kvflux_amd
+    from kvflux_amd import device
+
+    v3 = kvflux_amd.v3
+    N, CB = 4096, 65536
+    pool = v2.PhysicalBlockPool(N, 16)
+    gpu, cpu, nvme = v3.GpuTier(pool, CB), v3.CpuTier(N, CB), v3.NvmeTier(1, CB)
+    directory = v3.CacheDirectory(gpu, cpu, nvme)
+    store, host = v3.GpuChunkStore(N, CB), v3.PinnedChunkPool(N, CB)
+    xfer = v3.GpuCpuTransfer(directory, store, host)
+    keys = [v3.make_cache_key("bench", 1, v2.DType.BFloat16, 0, 1, [i]) for i in range(N)]
+    rng = np.random.default_rng(args.seed + 50)
+    for k in keys:
+        directory.create(k)
+    # scatter the host slots: take them in a random order
+    order = rng.permutation(N)
+    for i in order:
+        directory.place(keys[int(i)], v3.StorageTier.CPU)
+    for k in keys:
+        directory.place(k, v3.StorageTier.GPU)
+        directory.remove(k, v3.StorageTier.CPU)
+    base = store.device_ptr(v3.TierLocation(0, 0))  # slot 0: the start of the store
+    device.fill_random(base, N * CB // 2, 1, 0, args.seed + 51)
+    device.synchronize()
+    total = N * CB
+
+    xs = xfer.stream()
+
+    def move(batch, to_host, release=True, during=None):
+        """One direction for every key; returns the transfer stream's time (ms)
+        from the first copy to the last, and the decode time per step (ms)
+        when `during` launches decode steps meanwhile."""
+        e0, e1 = device.Event(), device.Event()
+        e0.record(xs)
+        if batch:
+            (xfer.begin_offload_batch if to_host else xfer.begin_onload_batch)(keys)
+        else:
+            for k in keys:
+                (xfer.begin_offload if to_host else xfer.begin_onload)(k)
+        e1.record(xs)
+        dec = during() if during else None
+        for k in keys:
+            (xfer.finish_offload if to_host else xfer.finish_onload)(k, release)
+        return e0.elapsed_ms(e1), dec
+
+    def decode_steps(n=10):
+        start, stop = device.Event(), device.Event()
+        start.record(stream)
+        for _ in range(n):
+            decode_launch()
+        stop.record(stream)
+        return start.elapsed_ms(stop) / n
+
+    res = {"chunks": N, "chunk_bytes": CB, "bytes": total, "decode_ms_alone": decode_ms}
+    first = device.memcpy_d2h(store.device_ptr(directory.at(keys[0]).gpu.location), CB, np.uint8)
+    for batch in (False, True):
+        move(batch, True), move(batch, False)  # warm
+        off, _ = move(batch, True)
+        on, _ = move(batch, False)
+        # the offload again, this time under decode steps on the compute stream
+        off_during, dec = move(batch, True, release=False, during=decode_steps)
+        for k in keys:  # back to GPU-only
+            directory.remove(k, v3.StorageTier.CPU)
+        res["batch_kernel" if batch else "dma_per_chunk"] = {
+            "offload_GBps": total / off / 1e6, "onload_GBps": total / on / 1e6,
+            "offload_GBps_during_decode": total / off_during / 1e6, "decode_ms_during_offload": dec}
+    again = device.memcpy_d2h(store.device_ptr(directory.at(keys[0]).gpu.location), CB, np.uint8)
+    res["round_trip_identical"] = bool(np.array_equal(first, again))
+    return res
 
 
 # --------------------------------------------------------------------- copy-on-write
@@ -545,6 +630,7 @@ def main() -> int:
         aux["cow"] = bench_cow(v2, args, stream.handle)
         log(f"cow {aux['cow']}")
         aux["decode_step"] = dec["decode_step"]
+        aux["offload"] = dec["offload"]
         for key in ("write", "gather_BFloat16", "gather_Float16", "cow"):
             aux[key]["pct_of_peak"] = round(100 * aux[key]["GBps"] / PEAK_HBM_GBPS, 2)
 
