@@ -731,7 +731,10 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
 #pragma unroll
         for (int kk = 0; kk < kSteps; ++kk) b.k[kk] = *reinterpret_cast<const uint4*>(kb + kk * 32);
 #pragma unroll
-        for (int i = 0; i < kVLoads; ++i) b.v[i] = *reinterpret_cast<const uint4*>(vb + i * 512);
+        // V rows arrive as whole 1 KiB lines per load: streamed (non-temporal).
+        // K loads take 64 bytes of each of 16 token rows, so a 128-byte line
+        // is completed by a second load and K keeps the default policy.
+        for (int i = 0; i < kVLoads; ++i) b.v[i] = stream_load(reinterpret_cast<const uint4*>(vb + i * 512));
     };
 
     // run_max is a reference point, not always the exact maximum: it only

@@ -24,7 +24,8 @@ namespace {
 constexpr int kCopyThreads = 512;
 constexpr std::uint64_t kPartBytes = 16384;  // bytes of a page per workgroup
 
-// Part blockIdx.y of an n-vector range: every load issued before the stores.
+// Part blockIdx.y of an n-vector range: every load issued before the stores,
+// both with the non-temporal hint (each byte moves once).
 template <typename Vec>
 __device__ inline void copy_part(const Vec* __restrict__ from, Vec* __restrict__ to, std::uint64_t n) {
     constexpr int kPer = static_cast<int>(kPartBytes / sizeof(Vec) / kCopyThreads);
@@ -33,12 +34,12 @@ __device__ inline void copy_part(const Vec* __restrict__ from, Vec* __restrict__
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
         const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
-        if (i < n) r[u] = from[i];
+        if (i < n) r[u] = stream_load(from + i);
     }
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
         const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
-        if (i < n) to[i] = r[u];
+        if (i < n) stream_store(to + i, r[u]);
     }
 }
 

@@ -11,7 +11,9 @@
 // lanes on consecutive 16-byte vectors (fully coalesced reads); each
 // (head, token) row lands as one contiguous row of the output. Only the
 // valid tokens of the tail page are touched. Every thread issues all of its
-// loads before its stores.
+// loads before its stores. Loads and stores carry the non-temporal hint:
+// each byte is read once and written once (measured on MI355X: 415 us
+// against 448 us for the 64-sequence BF16 batch).
 #include "common.h"
 
 namespace kvflux_hip {
@@ -58,11 +60,11 @@ __global__ __launch_bounds__(kThreads) void paged_kv_gather_kernel(
         const std::uint32_t token = row - head * block_size.divisor;
         live[u] = i < page_vectors && token < valid;
         dst[u] = ((out_token + token) * heads + head) * vpr + col;
-        if (live[u]) k[u] = src[src_base + i];
+        if (live[u]) k[u] = stream_load(src + src_base + i);
     }
 #pragma unroll
     for (int u = 0; u < kMaxPerThread; ++u) {
-        if (live[u]) out[dst[u]] = k[u];
+        if (live[u]) stream_store(out + dst[u], k[u]);
     }
 }
 
@@ -91,9 +93,9 @@ __global__ __launch_bounds__(kThreads) void paged_kv_gather_kernel_loop(
         if (token >= valid) continue;
         const std::uint64_t d = ((out_token + token) * heads + head) * vpr + col;
         if (blockIdx.z == 0) {
-            key_out[d] = key_cache[page * page_vectors + i];
+            stream_store(key_out + d, stream_load(key_cache + page * page_vectors + i));
         } else {
-            value_out[d] = value_cache[page * page_vectors + i];
+            stream_store(value_out + d, stream_load(value_cache + page * page_vectors + i));
         }
     }
 }
