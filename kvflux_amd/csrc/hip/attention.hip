@@ -170,9 +170,10 @@ struct Params {
     float* output;
     float* partial_acc;  // [rows][Hq][max_chunks][D]
     float* partial_ml;   // [rows][Hq][max_chunks][2]
-    std::uint32_t max_chunks;
+    std::uint32_t max_chunks;  // partial slots per (row, query head): ceil(kv_len / kChunk)
     std::uint32_t row_base;  // first row of this launch slice
     float scale_log2;        // log2(e) / sqrt(D)
+    std::uint32_t chunk_shift;  // block-size-16 kernel: log2(tokens per work item), 9..12
 };
 
 __device__ inline std::uint64_t row_length(const Params& p, std::uint32_t row) {
@@ -505,10 +506,14 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 
 // ---------------------------------------------------------------- block_size 16 decode
 // Hot path for 16-token pages, 16-bit caches, head_size 64/128:
-//  * persistent workgroups walk a plan of (row, 512-token chunk, kv head)
-//    items built in LDS from the row lengths (exclusive prefix of chunk
-//    counts), so no workgroup is launched for an empty chunk and consecutive
-//    items read the same pages for neighbouring kv heads;
+//  * persistent workgroups walk a plan of (row, chunk, kv head) items built
+//    in LDS from the row lengths (exclusive prefix of chunk counts), so no
+//    workgroup is launched for an empty chunk and consecutive items read the
+//    same pages for neighbouring kv heads. A chunk is 512..4096 tokens,
+//    chosen per call (the largest that leaves enough items to balance the
+//    persistent grid): fewer, longer items mean fewer item epilogues and
+//    fewer chunk partials (4096 against 512 tokens: 1.227 against 1.37 ms
+//    for 128 rows of U[1024, 32768] tokens on MI355X);
 //  * a 16-token tile is exactly one page: its id is one uniform LDS read and
 //    every K/V address is that page's base plus a constant lane offset, and
 //    both K and V of a tile arrive as fully coalesced 16-byte loads;
@@ -579,12 +584,19 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     constexpr int kRowStep = 64 / kCpr;     // token rows covered by one wave-wide load
     constexpr int kSwz = kCpr / 8;          // LDS slot swizzle multiplier
     constexpr int kSets = 3 * kG <= 16 ? 1 : 2;
-    constexpr int kTiles = kChunk / kBs;    // tiles per item
-    constexpr int kPerWave = kTiles / kWaves;
     constexpr int kRowBytes = kD * 2;
     constexpr int kQPer = (kG * kD + kThreads - 1) / kThreads;
     static_assert(kRowStep * kVLoads == kBs, "V tile covers 16 tokens");
-    static_assert(kPerWave % 2 == 0 && kPerWave <= 64, "tile pairs per wave");
+    // Chunk of 2^chunk_shift tokens (512..4096): 32..256 tiles per item, so
+    // 8..64 (even) tiles per wavefront, whose page offsets fit one lane each.
+    const std::uint32_t chunk_shift = p.chunk_shift;
+    const std::uint32_t chunk_tokens = 1u << chunk_shift;
+    const std::uint32_t tiles = chunk_tokens / kBs;  // tiles per item
+    const int per_wave = static_cast<int>(tiles / kWaves);
+    // ceil(len / chunk_tokens) without wrapping for len near 2^32.
+    auto chunks_of = [&](std::uint32_t len) {
+        return (len >> chunk_shift) + ((len & (chunk_tokens - 1)) != 0 ? 1u : 0u);
+    };
 
     __shared__ std::uint32_t plan[kPlanRows + 1];
     __shared__ std::uint32_t lens[kPlanRows];
@@ -609,7 +621,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             const std::uint64_t full = row_length(p, r);
             const std::uint32_t len = static_cast<std::uint32_t>(full < p.kv_len ? full : p.kv_len);
             lens[r] = len;
-            mine += len == 0 ? 1u : (len + kChunk - 1) / kChunk;
+            mine += len == 0 ? 1u : chunks_of(len);
         }
     }
     scan[tid] = mine;
@@ -626,7 +638,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             const std::uint32_t r = tid * kPer + i;
             if (r < rows) {
                 plan[r] = run;
-                run += lens[r] == 0 ? 1u : (lens[r] + kChunk - 1) / kChunk;
+                run += lens[r] == 0 ? 1u : chunks_of(lens[r]);
             }
         }
         if (tid == kThreads - 1) plan[rows] = scan[tid];
@@ -679,15 +691,15 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         it.row = uniform(lo);
         it.chunk = uniform(rc - plan[it.row]);
         const std::uint32_t len = lens[it.row];
-        const std::uint32_t begin = it.chunk * kChunk;
-        it.ntok = uniform(len > begin ? (len - begin < kChunk ? len - begin : kChunk) : 0u);
+        const std::uint32_t begin = it.chunk << chunk_shift;
+        it.ntok = uniform(len > begin ? (len - begin < chunk_tokens ? len - begin : chunk_tokens) : 0u);
         return it;
     };
-    // Lane j < kPerWave of every wave: element offset of the page of tile
+    // Lane j < per_wave of every wave: element offset of the page of tile
     // wave + kWaves * j, or kNoPage.
     auto fetch_pages = [&](const Item& it) -> std::uint64_t {
         const std::uint64_t* table_row = p.table + (p.seq_lens ? it.row : 0) * p.width;
-        const std::uint64_t logical = static_cast<std::uint64_t>(it.chunk) * kTiles + wave + kWaves * (lane % kPerWave);
+        const std::uint64_t logical = static_cast<std::uint64_t>(it.chunk) * tiles + wave + kWaves * (lane & (per_wave - 1));
         const std::uint64_t id = table_row[logical < p.width ? logical : p.width - 1];
         return logical < p.width && id < p.num_blocks ? id * page_stride : kNoPage;
     };
@@ -840,7 +852,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         }
     };
 
-    // ---- item loop. Wave w takes tiles w, w + 4, ... (kPerWave of them) of
+    // ---- item loop. Wave w takes tiles w, w + 4, ... (per_wave of them) of
     // every item; its loads run two tiles ahead through item boundaries. The
     // next item's page offsets and query are fetched at the start of the
     // current one.
@@ -892,15 +904,17 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             const std::uint32_t n = cur.ntok > begin ? (cur.ntok - begin < kBs ? cur.ntok - begin : kBs) : 0u;
             return page_of(cur_pages, j) == kNoPage ? 0u : n;
         };
-        auto issue = [&](int j, Tile& b) {  // stream position j: this item's tile j or the next item's j - kPerWave
-            if (j < kPerWave) {
+        auto issue = [&](int j, Tile& b) {  // stream position j: this item's tile j or the next item's j - per_wave
+            if (j < per_wave) {
                 load(page_of(cur_pages, j), cur.kvh, b);
             } else {
-                load(page_of(nxt_pages, j - kPerWave), nxt.kvh, b);
+                load(page_of(nxt_pages, j - per_wave), nxt.kvh, b);
             }
         };
-#pragma unroll
-        for (int j = 0; j < kPerWave; j += 2) {
+        // Two tiles per step, unrolled once more: a full unroll of 64 tiles
+        // would spill.
+#pragma unroll 2
+        for (int j = 0; j < per_wave; j += 2) {
             const Scores s0 = consume(valid_of(j), buf0);
             issue(j + 2, buf0);
             finish(s0);
@@ -935,7 +949,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         }
         __syncthreads();
 
-        const bool single = lens[cur.row] <= kChunk || p.max_chunks <= 1;
+        const bool single = lens[cur.row] <= chunk_tokens || p.max_chunks <= 1;
         const std::uint32_t qh0 = cur.kvh * kG;
         for (int idx = tid; idx < kG * kD; idx += kThreads) {
             const int g = idx / kD, d = idx % kD;
@@ -978,13 +992,14 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
 constexpr int kCombineThreads = 128;
 constexpr int kCombineMaxD = 256;  // largest head_size of the kernels that write partials
 
-__global__ __launch_bounds__(kCombineThreads) void paged_attention_combine_kernel(Params p, std::uint32_t head_dim) {
+__global__ __launch_bounds__(kCombineThreads) void paged_attention_combine_kernel(Params p, std::uint32_t head_dim,
+                                                                                   std::uint32_t chunk_tokens) {
     __shared__ float weight[kCombineThreads];
     __shared__ float wave_max_of[kCombineThreads / 64];
     const std::uint32_t row = p.row_base + blockIdx.x / p.query_heads;
     const std::uint32_t qh = blockIdx.x % p.query_heads;
     const std::uint64_t len = row_length(p, row);
-    const std::uint64_t needed = (len + kChunk - 1) / kChunk;
+    const std::uint64_t needed = (len + chunk_tokens - 1) / chunk_tokens;
     const std::uint32_t nchunks =
         needed < p.max_chunks ? static_cast<std::uint32_t>(needed) : p.max_chunks;
     if (nchunks <= 1) return;  // uniform over the block
@@ -1133,7 +1148,7 @@ int launch_split(Params p, std::uint64_t rows, std::uint64_t max_chunks, hipStre
         if (max_chunks > 1) {
             hipLaunchKernelGGL(paged_attention_combine_kernel,
                                dim3(static_cast<unsigned>(n * p.query_heads)), dim3(kCombineThreads), 0, s, p,
-                               static_cast<std::uint32_t>(kD));
+                               static_cast<std::uint32_t>(kD), static_cast<std::uint32_t>(kChunk));
             status = launch_status("paged_attention_combine_kernel");
             if (status != KVFLUX_OK) return status;
         }
@@ -1173,6 +1188,18 @@ int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s) {
         if (status != KVFLUX_OK) return status;
         slots = cus * (per_cu > 0 ? per_cu : 1);
     }
+    // Work item size: the largest chunk (512, 1024, 2048 or 4096 tokens)
+    // that still gives at least 8 items per resident workgroup when every
+    // row is kv_len long. Partial slots stay sized for 512-token chunks
+    // (max_chunks), an upper bound on the chunk count of any larger chunk.
+    std::uint32_t shift = 9;
+    while (shift < 12) {
+        const std::uint64_t wider = ((p.kv_len + (std::uint64_t{2} << shift) - 1) >> (shift + 1)) *
+                                    p.num_rows * p.heads;
+        if (wider < 8 * static_cast<std::uint64_t>(slots)) break;
+        ++shift;
+    }
+    p.chunk_shift = shift;
     const std::uint64_t items = static_cast<std::uint64_t>(p.num_rows) * max_chunks * p.heads;
     const unsigned grid = static_cast<unsigned>(items < static_cast<std::uint64_t>(slots) ? items : slots);
     p.row_base = 0;
@@ -1185,7 +1212,8 @@ int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s) {
                                         ? p.num_rows - base : 0x7fffffffULL / p.query_heads;
             p.row_base = static_cast<std::uint32_t>(base);
             hipLaunchKernelGGL(paged_attention_combine_kernel, dim3(static_cast<unsigned>(n * p.query_heads)),
-                               dim3(kCombineThreads), 0, s, p, static_cast<std::uint32_t>(kD));
+                               dim3(kCombineThreads), 0, s, p, static_cast<std::uint32_t>(kD),
+                               static_cast<std::uint32_t>(1u << p.chunk_shift));
             status = launch_status("paged_attention_combine_kernel");
             if (status != KVFLUX_OK) return status;
         }

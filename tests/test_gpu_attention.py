@@ -253,3 +253,65 @@ def test_shared_full_chunks_mixed_batch(gpu, v2, name, kv_heads, q_heads, head_s
     od2 = buffer_like(np.zeros(q.size, np.float32))
     v2.paged_attention_batch(storage, seqs, qd.ptr, od2.ptr, q_heads)
     assert np.array_equal(od2.download(np.float32).view(np.uint32), got.view(np.uint32))
+
+
+ITEM_CASES = [  # name, head_size, rows, max_len
+    ("BFloat16", 128, 128, 16384),
+    ("Float16", 128, 128, 32768),
+    ("BFloat16", 128, 256, 32768),
+    ("BFloat16", 64, 256, 16384),
+]
+
+
+@pytest.mark.parametrize("name,head_size,rows,max_len", ITEM_CASES)
+def test_decode_work_item_sizes(gpu, name, head_size, rows, max_len):
+    """The block-size-16 decode kernel splits rows into work items of 512 to
+    4096 tokens, the largest that leaves at least 8 items per resident
+    workgroup for rows of max_len tokens. With 2 kv heads on a 256-CU MI355X
+    (512 resident workgroups at head_size 128, 768 at 64) these batches take
+    1024-, 2048-, 4096- and 1024-token items. Rows map onto a small page pool
+    with repeats, so long rows need little memory; lengths sit on every item
+    boundary (and 0). Sampled rows match the oracle at 1e-5, and two calls
+    are bit-identical."""
+    lib = capi.lib()
+    H, Hq, bs, P = 2, 8, 16, 4096
+    code = DTYPES[name][0]
+    esize = 2
+    page = H * bs * head_size
+    kc = device.DeviceBuffer(P * page * esize)
+    vc = device.DeviceBuffer(P * page * esize)
+    device.fill_random(kc.ptr, P * page, code, 1, 31)
+    device.fill_random(vc.ptr, P * page, code, 1, 32)
+    rng = np.random.default_rng(rows + max_len)
+    edges = [0, 1, 15, 16, 17]
+    for c in (512, 1024, 2048, 4096, 8192):
+        edges += [c - 1, c, c + 1]
+    edges = [L for L in edges if L <= max_len] + [max_len - 1, max_len]
+    lens = np.concatenate([np.array(edges), rng.integers(1, max_len + 1, rows - len(edges))]).astype(np.uint64)
+    lens = lens[rng.permutation(rows)]
+    width = (max_len + bs - 1) // bs
+    table = rng.integers(0, P, (rows, width)).astype(np.uint64)
+    for r in range(rows):  # entries past the row's pages are never read: poison them
+        table[r, (int(lens[r]) + bs - 1) // bs:] = 2**64 - 1
+    td, ld = buffer_like(table.reshape(-1)), buffer_like(lens)
+    q = oracle.random_elements(0, rows * Hq * head_size, oracle.F32, 1, 33)
+    qd = buffer_like(q)
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_attention_workspace_size(rows, max_len, H, Hq, bs, head_size, C.byref(ws)))
+    wd = device.DeviceBuffer(max(ws.value, 256))
+    outs = []
+    for _ in range(2):
+        od = buffer_like(np.full(q.size, 7.0, np.float32))
+        capi.check(lib.kvflux_paged_attention(kc.ptr, vc.ptr, P, H, bs, head_size, code, td.ptr, width, ld.ptr,
+                                              max_len, rows, Hq, qd.ptr, od.ptr, wd.ptr, ws.value, None))
+        device.synchronize()
+        outs.append(od.download(np.float32))
+    got = outs[0].reshape(rows, Hq * head_size)
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    edge_rows = [int(np.flatnonzero(lens == L)[0]) for L in sorted(set(edges))]
+    sample = np.array(sorted(set(edge_rows) | set(rng.choice(rows, 8, replace=False).tolist())))
+    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table[sample].reshape(-1), width,
+                                      lens[sample], q.reshape(rows, -1)[sample].reshape(-1), Hq, threads=8)
+    assert np.abs(got[sample].reshape(-1) - exp).max() < TOL
