@@ -4,8 +4,12 @@
 // a row being a (query token, query head) pair of that kv head's group:
 // 256 / G tokens x G heads. Wavefront w owns row blocks 2w, 2w+1 of 16 rows
 // (row block b = head b % G, tokens 16 * (b / G) ..). Keys stream through
-// LDS in tiles of 64 (K and V, staged through registers so the next tile's
-// loads overlap this tile's MFMAs), processed as two halves of 32 keys:
+// LDS in tiles of 64, double-buffered: K and V go from global memory straight
+// into LDS (global_load_lds_dwordx4, no staging registers and no LDS write
+// instructions), the next tile's loads in flight while this tile is computed
+// (1.36 against 1.44 ms for 8 x 4096 tokens, 32/8 heads, D = 128 on MI355X,
+// where the LDS issue rate, about one instruction per 4.5 clocks per CU, is
+// a limit). Each tile is processed as two halves of 32 keys:
 //   S^T = K Q^T    v_mfma_f32_16x16x32 (A = K rows from LDS, B = Q rows held
 //                  in registers, rounded to the cache dtype with the
 //                  softmax scale folded in)
@@ -72,13 +76,17 @@ __device__ inline float max_across_quads(float x) {
 
 constexpr int kPfThreads = 512;   // 8 wavefronts, two per SIMD
 constexpr int kPfWaves = kPfThreads / 64;
-constexpr int kPfRows = 256;      // rows per workgroup
-constexpr int kPfNt = kPfRows / 16 / kPfWaves;  // 16-row blocks per wavefront
+constexpr int kPfNt = 2;          // 16-row blocks per wavefront
+constexpr int kPfRows = kPfWaves * kPfNt * 16;  // rows per workgroup
 constexpr int kPfTile = 64;       // keys per LDS tile
 constexpr int kPfTableMax = 2048; // page ids held in LDS (kv_len <= 2048 * block_size)
-// Flag bit of a missing page in the LDS page list (ids are below 2^31): it is
-// loaded from page 0 (never out of bounds) and its K and V staged as zeros.
+// Flag bit of a missing page in the LDS page list (ids are below 2^31): its
+// K and V rows are loaded from pf_zero_rows instead.
 constexpr std::uint32_t kPfMissing = 0x80000000u;
+// One head's rows of one page at block_size <= 64 and head_size <= 128
+// (16-bit elements): the source of missing pages, all zeros.
+constexpr int kPfZeroBytes = 64 * 256;
+__device__ __attribute__((aligned(16))) unsigned char pf_zero_rows[kPfZeroBytes];
 
 struct PrefillParams {
     const void* key_cache;
@@ -97,6 +105,41 @@ struct PrefillParams {
     float scale_log2;         // log2(e) / sqrt(D)
 };
 
+// s_waitcnt immediates (gfx9 encoding): vmcnt(n) alone, lgkmcnt(0) alone.
+template <int kN>
+__device__ inline void wait_vm() {
+    static_assert(kN >= 0 && kN < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((kN & 15) | ((kN >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4)); }
+// One 16-byte-per-lane load from global memory straight into LDS at
+// m0 + lane * 16 (m0 wave-uniform). Issued as inline assembly so the
+// compiler's wait-count tracking does not treat it as an LDS write (it would
+// then wait for every such load before any LDS read); completion is ordered
+// by the explicit vmcnt waits before the barriers.
+__device__ inline void load_to_lds(const void* src, std::uint32_t lds_byte) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_byte) : "memory");
+}
+__device__ inline std::uint32_t lds_address(const void* p) {
+    return static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>((__attribute__((address_space(3))) const char*)p));
+}
+// Workgroup barrier without the release fence of __syncthreads (which would
+// also wait for the tile loads still in flight); LDS visibility is ordered by
+// the explicit waits before it.
+__device__ inline void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+// Wave priority (s_setprio) pinned in place: raised while a wave issues its
+// QK^T MFMAs, so a SIMD's other wave runs its softmax in the meantime.
+template <short kLevel>
+__device__ inline void set_priority() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(kLevel);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <typename E, int kD, int kG>
 __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams p) {
     using M = E;
@@ -105,39 +148,36 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     constexpr int kDt = kD / 16;               // dim blocks of O^T
     constexpr int kCpr = kD / 8;               // 16-byte chunks per key row
     constexpr int kRowBytes = kD * 2;
-    constexpr int kTileChunks = kPfTile * kCpr;
-    constexpr int kChunksPerThread = kTileChunks / kPfThreads;
+    constexpr int kTileBytes = kPfTile * kRowBytes;
+    constexpr int kDma = kTileBytes / (kPfThreads * 16);  // tile loads per thread per cache
     constexpr int kTok = kPfRows / kG;         // query tokens per workgroup
     constexpr int kVSwz = kCpr / 8;            // V slot swizzle multiplier
     constexpr float kLazy = 8.0f;
-    static_assert(kChunksPerThread >= 1 && kTileChunks % kPfThreads == 0, "tile split");
+    static_assert(kDma >= 1 && kTileBytes % (kPfThreads * 16) == 0, "tile split");
+    static_assert(kPfRows % (16 * kG) == 0, "whole token blocks per workgroup");
 
-    __shared__ __attribute__((aligned(16))) std::uint16_t ktile[kPfTile * kD];
-    __shared__ __attribute__((aligned(16))) std::uint16_t vtile[kPfTile * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t ktile0[kPfTile * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t ktile1[kPfTile * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t vtile0[kPfTile * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t vtile1[kPfTile * kD];
     __shared__ std::uint32_t pages[kPfTableMax];
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int col = lane % 16, quad = lane / 16;
-    // Heaviest query blocks (most keys) first.
     const std::uint32_t kvh = blockIdx.x % p.heads;
     const std::uint32_t qb = p.qblocks - 1 - blockIdx.x / p.heads;
     const std::uint32_t t0 = qb * kTok;
     const std::uint32_t t_end = t0 + kTok < p.tq ? t0 + kTok : p.tq;
-    const std::uint32_t past = p.kv_len - p.tq;  // keys before the first query
+    const std::uint32_t past = p.kv_len - p.tq;
     const std::uint32_t last_key = past + t_end - 1;
     const std::uint32_t ntiles = last_key / kPfTile + 1;
     const std::uint32_t npages = ((ntiles * kPfTile - 1) >> p.bs_shift) + 1;
-    // Page ids of the tiles; a missing page (past the table or kv_len, or an
-    // id >= num_blocks) is loaded from page 0 and zeroed before it reaches LDS.
-    bool missing = false;
     for (std::uint32_t i = tid; i < npages; i += kPfThreads) {
         const std::uint64_t id = i < p.table_len ? p.table[i] : p.num_blocks;
         const bool ok = id < p.num_blocks && (static_cast<std::uint64_t>(i) << p.bs_shift) < p.kv_len;
         pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
-        missing |= !ok && (static_cast<std::uint64_t>(i) << p.bs_shift) < p.kv_len;
     }
 
-    // Q rows of this wave: B operands [row block][K step], already scaled.
     Vec qb_op[kPfNt][kSteps];
     std::uint32_t row_token[kPfNt];
 #pragma unroll
@@ -155,147 +195,123 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             std::uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                w[e] = M::pack(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2);
-            }
+            for (int e = 0; e < 4; ++e) w[e] = M::pack(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2);
             qb_op[n][kk] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
         }
     }
-    // pages[] ready; uniform: some page inside kv_len is missing
-    const bool table_gaps = __syncthreads_or(missing);
+    __syncthreads();  // pages[] ready (the query loads are complete as well)
 
-    // Tile staging: chunk id = tid + kPfThreads * i; row = id / kCpr, c = id % kCpr.
-    // A tile starts on a page boundary (block_size divides 64), so a thread's
-    // row sits at a fixed offset in its page, and its page is entry
-    // tile * (64 / block_size) + row / block_size of pages[].
+    // Tile loads straight into LDS: load i of a wavefront fills bytes
+    // [1 KiB * (i * waves + wave), +1 KiB) of the tile, lane l the 16 bytes
+    // at l * 16 of that: LDS chunk e = row * kCpr + slot. The swizzle is set
+    // by which global chunk a lane fetches: K chunk slot ^ kswz(row), V chunk
+    // slot ^ vswz(row), so reads below see the swizzled layout.
     const char* kc = static_cast<const char*>(p.key_cache);
     const char* vc = static_cast<const char*>(p.value_cache);
     const std::uint32_t page_bytes = (static_cast<std::uint32_t>(kRowBytes) << p.bs_shift) * p.heads;
+    const std::uint32_t head_bytes = (kvh << p.bs_shift) * kRowBytes;
     const std::uint32_t tile_pages_shift = 6 - p.bs_shift;
-    std::uint32_t lane_bytes[kChunksPerThread], row_page[kChunksPerThread];
+    const std::uint32_t in_page_mask = (1u << p.bs_shift) - 1;
+    auto kswz = [](int row) { return kCpr == 16 ? (row & 15) : ((row >> 1) & 7); };
+    auto vswz = [](int row) { return kVSwz * (row & 7); };
+    auto issue = [&](std::uint32_t tile, auto buf) {
 #pragma unroll
-    for (int i = 0; i < kChunksPerThread; ++i) {
-        const int id = tid + kPfThreads * i;
-        const int row = id / kCpr, c = id % kCpr;
-        row_page[i] = static_cast<std::uint32_t>(row) >> p.bs_shift;
-        lane_bytes[i] = ((kvh << p.bs_shift) + (static_cast<std::uint32_t>(row) & ((1u << p.bs_shift) - 1))) *
-                            kRowBytes + c * 16;
-    }
-    auto k_slot = [](int row, int c) {  // conflict-free for 16-row ds_read_b128
-        return kCpr == 16 ? (c ^ (row & 15)) : (c ^ ((row >> 1) & 7));
-    };
-    auto v_slot = [](int row, int c) { return c ^ (kVSwz * (row & 7)); };
-    struct Staged {
-        uint4 k[kChunksPerThread], v[kChunksPerThread];
-    };
-    // Unconditional loads (straight-line code keeps the wait counts exact).
-    auto fetch = [&](std::uint32_t tile, Staged& st) {
-#pragma unroll
-        for (int i = 0; i < kChunksPerThread; ++i) {
-            const std::uint32_t page = pages[(tile << tile_pages_shift) + row_page[i]] & ~kPfMissing;
-            const std::uint64_t off = static_cast<std::uint64_t>(page) * page_bytes + lane_bytes[i];
-            st.k[i] = *reinterpret_cast<const uint4*>(kc + off);
-            st.v[i] = *reinterpret_cast<const uint4*>(vc + off);
-        }
-    };
-    auto stage = [&](std::uint32_t tile, const Staged& st) {
-        char* kb = reinterpret_cast<char*>(ktile);
-        char* vb = reinterpret_cast<char*>(vtile);
-        // Keys at or past kv_len, or on a missing page, are staged as zeros
-        // (finite V under a zero weight). Uniform test: only the last tile or
-        // a table with gaps takes it. The loaded registers are only read
-        // here, never overwritten, so no wait is needed for the other set.
-        const bool fix = table_gaps || (tile + 1) * kPfTile > p.kv_len;
-#pragma unroll
-        for (int i = 0; i < kChunksPerThread; ++i) {
-            const int id = tid + kPfThreads * i;
-            const int row = id / kCpr, c = id % kCpr;
-            uint4 k = st.k[i], v = st.v[i];
-            if (fix) {
-                const std::uint32_t key = tile * kPfTile + row;
-                const std::uint32_t missing_bit = pages[(tile << tile_pages_shift) + row_page[i]] & kPfMissing;
-                const std::uint32_t keep = ((key >= p.kv_len) | (missing_bit != 0)) ? 0u : ~0u;
-                k = make_uint4(k.x & keep, k.y & keep, k.z & keep, k.w & keep);
-                v = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+        for (int i = 0; i < kDma; ++i) {
+            const int e = (i * kPfWaves + wave) * 64 + lane;
+            const int row = e / kCpr, slot = e % kCpr;
+            const std::uint32_t r = static_cast<std::uint32_t>(row) & in_page_mask;
+            const std::uint32_t entry = pages[(tile << tile_pages_shift) + (static_cast<std::uint32_t>(row) >> p.bs_shift)];
+            const std::uint32_t kchunk = (slot ^ kswz(row)) * 16, vchunk = (slot ^ vswz(row)) * 16;
+            const char* ks;
+            const char* vs;
+            if (entry & kPfMissing) {
+                ks = reinterpret_cast<const char*>(pf_zero_rows) + r * kRowBytes + kchunk;
+                vs = reinterpret_cast<const char*>(pf_zero_rows) + r * kRowBytes + vchunk;
+            } else {
+                const std::uint64_t base = static_cast<std::uint64_t>(entry) * page_bytes + head_bytes + r * kRowBytes;
+                ks = kc + base + kchunk;
+                vs = vc + base + vchunk;
             }
-            *reinterpret_cast<uint4*>(kb + row * kRowBytes + k_slot(row, c) * 16) = k;
-            *reinterpret_cast<uint4*>(vb + row * kRowBytes + v_slot(row, c) * 16) = v;
+            const std::uint32_t dst = static_cast<std::uint32_t>((i * kPfWaves + wave) * 1024);
+            const std::uint32_t kdst = (decltype(buf)::value == 0 ? lds_address(ktile0) : lds_address(ktile1)) + dst;
+            const std::uint32_t vdst = (decltype(buf)::value == 0 ? lds_address(vtile0) : lds_address(vtile1)) + dst;
+            load_to_lds(ks, __builtin_amdgcn_readfirstlane(kdst));
+            load_to_lds(vs, __builtin_amdgcn_readfirstlane(vdst));
         }
     };
-    // Transposing V^T reads: lane (q, s) addresses key row 4q + s/4 (+16 for
-    // the second half of the operand), dims 16*dt + 4*(s%4). The swizzle
-    // acts on bits 4..6 of the byte offset and dt on bits 5..7, so block dt
-    // is v_read0 ^ (dt << 5); row offsets of whole tiles are immediates.
-    std::uint32_t v_rd[kDt];
+    // Keys at or past kv_len of the last tile: their V rows are zeroed (a
+    // finite value under a zero weight), each thread its own loaded chunks,
+    // after its loads have landed.
+    auto zero_tail = [&](std::uint32_t tile, std::uint16_t* vt) {
+#pragma unroll
+        for (int i = 0; i < kDma; ++i) {
+            const int e = (i * kPfWaves + wave) * 64 + lane;
+            const std::uint32_t key = tile * kPfTile + static_cast<std::uint32_t>(e / kCpr);
+            if (key >= p.kv_len) *reinterpret_cast<uint4*>(reinterpret_cast<char*>(vt) + e * 16) = make_uint4(0, 0, 0, 0);
+        }
+    };
+
+    // V^T block dt: v_read0 ^ (dt << 5); K step kk: k_read0 ^ (kk << 6)
+    // (chunk quad + 4 * kk = quad ^ 4 * kk of row col; 64 * kk < kRowBytes).
+    std::uint32_t v_read0;
     {
         const int s = lane % 16, r = 4 * quad + s / 4;
         const int c = (4 * (s % 4)) / 8;
-        const std::uint32_t v_read0 = r * kRowBytes + (v_slot(r, c) * 16) + (s % 2) * 8;
-#pragma unroll
-        for (int dt = 0; dt < kDt; ++dt) v_rd[dt] = v_read0 ^ (dt << 5);
+        v_read0 = r * kRowBytes + ((c ^ vswz(r)) * 16) + (s % 2) * 8;
     }
-    // K A operand of lane (quad, col) for step kk: key row 16*m + col (the
-    // K swizzle depends on the row only through col), 16-byte column
-    // quad + 4*kk.
-    std::uint32_t k_rd[kSteps];
-#pragma unroll
-    for (int kk = 0; kk < kSteps; ++kk) k_rd[kk] = col * kRowBytes + k_slot(col, quad + 4 * kk) * 16;
+    const std::uint32_t k_read0 = col * kRowBytes + (quad ^ kswz(col)) * 16;
 
     pf_f32x4_t acc[kDt][kPfNt];
 #pragma unroll
     for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
         for (int n = 0; n < kPfNt; ++n) acc[dt][n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    // Per row block: the row sums of the rounded weights (an MFMA against a
-    // matrix of ones, so every entry holds its column's sum) and minus the
-    // row's reference point, broadcast: the S^T accumulators start from it,
-    // so the scores arrive already shifted.
-    pf_f32x4_t lsum[kPfNt], nref[kPfNt];
+    pf_f32x4_t lsum[kPfNt];
+    float nref[kPfNt];  // minus the row's reference point (equal in the four quads of a column)
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
         lsum[n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        nref[n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        nref[n] = 0.0f;
     }
-    bool have_ref = false;  // uniform: false until the first half-tile sets every row's reference
+    bool have_ref = false;
     const Vec ones = __builtin_bit_cast(Vec, make_uint4(M::kOnes, M::kOnes, M::kOnes, M::kOnes));
-    const std::uint32_t min_limit = past + t0;  // smallest causal limit of the block
+    const std::uint32_t min_limit = past + t0;
 
-    // Tiles alternate between two register sets, loaded two tiles ahead.
-    auto compute_tile = [&](std::uint32_t tile) {
+    auto compute_tile = [&](std::uint32_t tile, const std::uint16_t* kt, const std::uint16_t* vt) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const std::uint32_t k0 = tile * kPfTile + 32 * h;
             if (k0 > last_key) break;  // uniform
-            // S^T - ref for keys k0 .. k0+31: two 16-key tiles x the row blocks.
             pf_f32x4_t s[2][kPfNt];
+            set_priority<1>();
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
+            for (int kt2 = 0; kt2 < 2; ++kt2) {
                 Vec a[kSteps];
 #pragma unroll
                 for (int kk = 0; kk < kSteps; ++kk) {
                     a[kk] = __builtin_bit_cast(
-                        Vec, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(ktile) +
-                                                             (32 * h + 16 * kt) * kRowBytes + k_rd[kk]));
+                        Vec, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(kt) +
+                                                             (32 * h + 16 * kt2) * kRowBytes + (k_read0 ^ (kk << 6))));
                 }
 #pragma unroll
                 for (int n = 0; n < kPfNt; ++n) {
-                    pf_f32x4_t x = nref[n];
+                    pf_f32x4_t x = pf_f32x4_t{nref[n], nref[n], nref[n], nref[n]};
 #pragma unroll
                     for (int kk = 0; kk < kSteps; ++kk) x = M::mma(a[kk], qb_op[n][kk], x);
-                    s[kt][n] = x;
+                    s[kt2][n] = x;
                 }
             }
-            if (k0 + 31 > min_limit) {  // uniform; keys past the row's causal limit
+            set_priority<0>();
+            if (k0 + 31 > min_limit) {
 #pragma unroll
                 for (int n = 0; n < kPfNt; ++n) {
                     const std::int32_t room = static_cast<std::int32_t>(past + row_token[n] - k0 - 4 * quad);
 #pragma unroll
-                    for (int kt = 0; kt < 2; ++kt)
+                    for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) s[kt][n][r] = 16 * kt + r > room ? -INFINITY : s[kt][n][r];
+                        for (int r = 0; r < 4; ++r) s[kt2][n][r] = 16 * kt2 + r > room ? -INFINITY : s[kt2][n][r];
                 }
             }
-            // Row maxima relative to the reference (equal in the four quads of a column).
             float tmax[kPfNt];
             bool grow = !have_ref;
 #pragma unroll
@@ -305,19 +321,15 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                                                 max3(s[1][n][2], s[1][n][3], -INFINITY)));
                 grow |= tmax[n] > kLazy;
             }
-            // Rare, wave-uniform: move the reference of the rows whose maximum
-            // exceeds it by more than 2^kLazy (all rows on the first half-tile)
-            // and rescale what they have accumulated.
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {
 #pragma unroll
                 for (int n = 0; n < kPfNt; ++n) {
                     const float shift = !have_ref || tmax[n] > kLazy ? tmax[n] : 0.0f;
-                    // min(.., 0): on the first half-tile the accumulators are still zero
                     const float alpha = __builtin_amdgcn_exp2f(fminf(-shift, 0.0f));
                     nref[n] -= shift;
                     lsum[n] *= alpha;
 #pragma unroll
-                    for (int kt = 0; kt < 2; ++kt) s[kt][n] -= shift;
+                    for (int kt2 = 0; kt2 < 2; ++kt2) s[kt2][n] -= shift;
 #pragma unroll
                     for (int dt = 0; dt < kDt; ++dt) acc[dt][n] *= alpha;
                 }
@@ -328,18 +340,17 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             for (int n = 0; n < kPfNt; ++n) {
                 std::uint32_t w[4];
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt) {
-                    w[2 * kt] = M::pack(__builtin_amdgcn_exp2f(s[kt][n][0]), __builtin_amdgcn_exp2f(s[kt][n][1]));
-                    w[2 * kt + 1] = M::pack(__builtin_amdgcn_exp2f(s[kt][n][2]), __builtin_amdgcn_exp2f(s[kt][n][3]));
+                for (int kt2 = 0; kt2 < 2; ++kt2) {
+                    w[2 * kt2] = M::pack(__builtin_amdgcn_exp2f(s[kt2][n][0]), __builtin_amdgcn_exp2f(s[kt2][n][1]));
+                    w[2 * kt2 + 1] = M::pack(__builtin_amdgcn_exp2f(s[kt2][n][2]), __builtin_amdgcn_exp2f(s[kt2][n][3]));
                 }
                 pb[n] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
             }
-            // O^T += V^T P^T for the 32 keys of this half; l += 1 P^T.
             const auto* vbase = (__attribute__((address_space(3))) char*)(
-                (__attribute__((address_space(3))) std::uint16_t*)vtile);
+                (__attribute__((address_space(3))) std::uint16_t*)vt);
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
-                const std::uint32_t off = v_rd[dt] + 32 * h * kRowBytes;
+                const std::uint32_t off = (v_read0 ^ (dt << 5)) + 32 * h * kRowBytes;
                 const pf_i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off));
                 const pf_i16x4_t hi =
                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off + 16 * kRowBytes));
@@ -351,29 +362,41 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             for (int n = 0; n < kPfNt; ++n) lsum[n] = M::mma(ones, pb[n], lsum[n]);
         }
     };
-    // Every fetch is issued, past the end as a reload of the last tile, so
-    // the loads form one in-order stream and each stage() waits only for the
-    // set it writes (the other set stays in flight).
-    const std::uint32_t last_tile = ntiles - 1;
-    auto clamp_tile = [last_tile](std::uint32_t t) { return t < last_tile ? t : last_tile; };
-    Staged set0, set1;
-    fetch(0, set0);
-    fetch(clamp_tile(1), set1);
+
+    // Two LDS tile buffers: tile t lives in buffer t % 2. The loads of tile
+    // t + 1 are issued before tile t is computed; each step waits for its own
+    // tile's loads (2 * kDma per thread, issued one step earlier), then a
+    // barrier publishes the tile; a second barrier frees the buffer.
+    const bool tail = ntiles * kPfTile > p.kv_len;  // the last tile has keys past kv_len
+    issue(0, std::integral_constant<int, 0>{});
     for (std::uint32_t tile = 0; tile < ntiles; tile += 2) {
-        stage(tile, set0);
-        __syncthreads();
-        fetch(clamp_tile(tile + 2), set0);
-        compute_tile(tile);
-        __syncthreads();  // the tile is consumed before the next stage()
+        if (tile + 1 < ntiles) {
+            issue(tile + 1, std::integral_constant<int, 1>{});
+            wait_vm<2 * kDma>();
+        } else {
+            wait_vm<0>();
+        }
+        if (tail && tile + 1 == ntiles) zero_tail(tile, vtile0);
+        wait_lgkm0();
+        lds_barrier();
+        compute_tile(tile, ktile0, vtile0);
+        wait_lgkm0();
+        lds_barrier();
         if (tile + 1 >= ntiles) break;
-        stage(tile + 1, set1);
-        __syncthreads();
-        fetch(clamp_tile(tile + 3), set1);
-        compute_tile(tile + 1);
-        __syncthreads();
+        if (tile + 2 < ntiles) {
+            issue(tile + 2, std::integral_constant<int, 0>{});
+            wait_vm<2 * kDma>();
+        } else {
+            wait_vm<0>();
+        }
+        if (tail && tile + 2 == ntiles) zero_tail(tile + 1, vtile1);
+        wait_lgkm0();
+        lds_barrier();
+        compute_tile(tile + 1, ktile1, vtile1);
+        wait_lgkm0();
+        lds_barrier();
     }
 
-    // O = O^T / l.
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
         const float l = lsum[n][0];
@@ -394,9 +417,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 
 template <typename E, int kD>
 int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_t s) {
-    const unsigned grid_of[9] = {0, kPfRows / 1, kPfRows / 2, 0, kPfRows / 4, 0, 0, 0, kPfRows / 8};
     PrefillParams q = p;
-    q.qblocks = (p.tq + grid_of[group] - 1) / grid_of[group];
+    const unsigned tok = kPfRows / group;
+    q.qblocks = (p.tq + tok - 1) / tok;
     const dim3 grid(q.qblocks * p.heads);
     switch (group) {
     case 1: hipLaunchKernelGGL((paged_prefill_kernel<E, kD, 1>), grid, dim3(kPfThreads), 0, s, q); break;

@@ -149,3 +149,39 @@ def test_prefill_through_cpp_layer(gpu, v2):
     exp = oracle.paged_attention_causal(kh, vh, 2, 16, 128, oracle.BF16, v2.build_read_block_table(seq), 500, q,
                                         500, 8, threads=8)
     assert np.abs(got - exp).max() < 2e-2
+
+
+GAP_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens, missing table entries
+    ("BFloat16", 2, 8, 128, 4, 500, 500, [3, 40, 124]),
+    ("Float16", 1, 8, 64, 8, 333, 120, [0, 20, 41]),
+    ("BFloat16", 2, 4, 128, 1, 130, 130, [7, 129]),
+]
+
+
+@pytest.mark.parametrize("name,kv_heads,q_heads,head_size,bs,kv_len,q_tokens,missing", GAP_CASES)
+def test_prefill_small_pages_and_missing_ids(gpu, name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens,
+                                             missing):
+    """Block sizes below 16 (a 64-key tile spans 16 to 64 pages) and table
+    entries that are not pages of the pool: such a page reads as zeros for K
+    and V. The references see the same cache with one all-zero page appended
+    and the missing entries pointing at it."""
+    blocks = (kv_len + bs - 1) // bs + 17
+    seed = kv_len + q_tokens + bs
+    kc, vc, table = setup_case(name, blocks, kv_heads, bs, head_size, kv_len, seed)
+    table = table.copy()
+    table[missing] = 2**64 - 1
+    q = oracle.random_elements(0, q_tokens * q_heads * head_size, oracle.F32, 1, seed)
+    got = run_prefill(name, kc, vc, blocks, kv_heads, bs, head_size, table, kv_len, q, q_tokens, q_heads)
+    assert np.all(np.isfinite(got))
+    page = kv_heads * bs * head_size
+    kh = np.concatenate([kc.download(np.uint16), np.zeros(page, np.uint16)])
+    vh = np.concatenate([vc.download(np.uint16), np.zeros(page, np.uint16)])
+    ref_table = table.copy()
+    ref_table[missing] = blocks  # the appended zero page
+    exp = oracle.paged_attention_causal(kh, vh, kv_heads, bs, head_size, CODES[name], ref_table, kv_len, q,
+                                        q_tokens, q_heads, threads=8)
+    assert np.abs(got - exp).max() < 2e-2
+    rows = sorted({0, 1, q_tokens // 2, q_tokens - 2, q_tokens - 1} & set(range(q_tokens)))
+    emu = emulate(kh, vh, name, kv_heads, bs, head_size, ref_table, kv_len, q, q_tokens, q_heads, rows)
+    sub = got.reshape(q_tokens, q_heads, head_size)[rows]
+    assert np.abs(sub - emu).max() < 4e-3
