@@ -23,7 +23,11 @@ Also measured in the same run (sub-objects of the JSON line):
   offload: GPU <-> CPU chunk transfer (tiered cache), per-chunk DMA against
            one kernel per batch, and overlap with the decode kernel
   cpu_baseline : the CPU oracle (gather + double-precision attention, one
-           thread) on a bounded sample of the decode rows, timed here.
+           thread) on a bounded sample of the decode rows, timed here; the
+           same rows on all cores of the process's CPU share (at most 16) in
+           `all_cores`, and the CPU model.
+  write, gather and prefill also report the synchronous C++ API time
+  (`api_us` / `api_ms`: validation, metadata upload, launch, synchronisation).
 
 roofline.traffic is the HBM traffic of one decode call measured with
 rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by what the same counters read
@@ -53,6 +57,16 @@ PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
 TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_bs16_traffic.txt"
 METRIC = "decode paged-attn HBM TB/s (% of peak) + KV write/gather GB/s, 1 GPU"
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def log(*a):
@@ -155,6 +169,7 @@ def bench_decode(v2, args, stream):
     err = 0.0
     cpu_s = 0.0
     cpu_bytes = 0
+    compact = []
     for r in sample_rows:
         L = int(lens[r])
         npg = (L + bs - 1) // bs
@@ -171,6 +186,17 @@ def bench_decode(v2, args, stream):
         cpu_s += time.perf_counter() - t0
         cpu_bytes += L * kv_token_bytes
         err = max(err, float(np.abs(ref - out[r * Hq * D:(r + 1) * Hq * D]).max()))
+        compact.append((kc, vc, local, npg, L, r))
+    # The same rows on all cores of this process's CPU share (at most 16, the
+    # share of one GPU): the oracle splits each row's query heads over threads.
+    threads = min(16, len(os.sched_getaffinity(0)))
+    cpu_mt_s = 0.0
+    for kc, vc, local, npg, L, r in compact:
+        t0 = time.perf_counter()
+        oracle.paged_attention_rows(kc, vc, H, bs, D, oracle.BF16, local, npg, np.array([L], np.uint64), qh[r], Hq,
+                                    threads=threads)
+        cpu_mt_s += time.perf_counter() - t0
+    del compact
     step = None if args.skip_aux else bench_decode_step(v2, args, storage, seqs, width, ms)
     offload = None if args.skip_aux else bench_offload(v2, args, launch, stream, ms)
     del seqs, base
@@ -185,7 +211,8 @@ def bench_decode(v2, args, stream):
         "max_abs_err": err,
         "cpu": None if not sample_rows else
                {"value": cpu_bytes / cpu_s / 1e12, "unit": "TB/s", "cores": 1, "kind": "port",
-                "seconds": cpu_s,
+                "seconds": cpu_s, "cpu_model": cpu_model(),
+                "all_cores": {"value": cpu_bytes / cpu_mt_s / 1e12, "cores": threads, "seconds": cpu_mt_s},
                 "sample": f"{len(sample_rows)} decode rows (L={[int(lens[r]) for r in sample_rows]}, "
                           "32 q heads each): page gather + double-precision softmax attention, 1 thread"},
     }
@@ -464,6 +491,14 @@ def bench_gather(v2, args, stream, dtype_name: str):
                                               ld.ptr, od.ptr, S, max_len, ko.ptr, vo.ptr, stream))
 
     ms = time_launches(launch, stream, args.warmup, args.steps)
+    # The synchronous C++ API on the same batch (validation, metadata upload,
+    # one launch, stream synchronisation).
+    v2.read_paged_kv_batch(storage, seqs, ko.ptr, vo.ptr)
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        v2.read_paged_kv_batch(storage, seqs, ko.ptr, vo.ptr)
+    api_us = (time.perf_counter() - t0) / reps * 1e6
     # Bit-exact check of a few sequences against the oracle gather.
     page_elems = H * bs * D
     mism = 0
@@ -483,7 +518,7 @@ def bench_gather(v2, args, stream, dtype_name: str):
     bytes_step = 8192 * total + 8 * pages
     del seqs
     return {"dtype": dtype_name, "kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9,
-            "bytes": bytes_step, "tokens": total, "mismatched_elements_sampled": mism}
+            "bytes": bytes_step, "api_us": api_us, "tokens": total, "mismatched_elements_sampled": mism}
 
 
 # --------------------------------------------------------------------- prefill
@@ -520,6 +555,15 @@ def bench_prefill(v2, args, stream):
                                                 npages, T, T, Hq, qs[i].ptr, out.ptr + i * T * Hq * D * 4, stream))
 
     ms = time_launches(launch, stream, max(1, args.warmup // 2), max(3, args.steps // 4))
+    # The synchronous C++ API (paged_attention with AttentionPrecision::Fast,
+    # one call per sequence) on the same inputs.
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for i in range(S):
+            v2.paged_attention(storage, seqs[i], qs[i].ptr, out.ptr + i * T * Hq * D * 4, T, Hq,
+                               v2.AttentionPrecision.Fast)
+    api_ms = (time.perf_counter() - t0) / reps * 1e3
     flops = S * T * (T + 1) / 2 * Hq * D * 4
     # The last queries (longest rows) of the first and last sequence against the CPU reference.
     page_bytes = H * bs * D * 2
@@ -539,7 +583,7 @@ def bench_prefill(v2, args, stream):
     del seqs
     tflops = flops / (ms * 1e-3) / 1e12
     return {"workload": "8 x 4096-token causal prefill, 32 q / 8 kv heads, D=128, BF16 KV, block_size 16",
-            "kernel": "paged_prefill_kernel<bf16,128,4>", "ms": ms, "TFLOPs": tflops,
+            "kernel": "paged_prefill_kernel<bf16,128,4>", "ms": ms, "api_ms": api_ms, "TFLOPs": tflops,
             "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS, "flops": flops,
             "max_abs_err_vs_oracle": err, "rows_checked": checked, "tolerance": 2e-2}
 
