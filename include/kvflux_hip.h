@@ -137,9 +137,12 @@ int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
  * workspace: device scratch of at least kvflux_paged_attention_workspace_size()
  *   bytes (no initialisation needed). Calls that share a workspace must be
  *   ordered (same stream).
- * Rows longer than one 512-token split take two launches: the split kernel
- * and a combine kernel that merges the split partials in ascending split
- * order, so results are deterministic.
+ * Rows longer than one split take two launches: the split kernel and a
+ * combine kernel that merges the split partials in ascending split order, so
+ * results are deterministic. A split is 512 tokens; the block-size-16 kernel
+ * (16-bit caches, head_size 64/128) uses 512 to 4096 tokens, the largest that
+ * leaves 8 work items per resident workgroup for num_rows rows of kv_len
+ * tokens. The workspace is sized for 512-token splits, enough for either.
  * ------------------------------------------------------------------------- */
 int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t kv_len,
                                           uint64_t num_kv_heads, uint64_t query_heads,

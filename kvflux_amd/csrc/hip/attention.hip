@@ -1225,7 +1225,10 @@ template <typename E, int kD>
 int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint64_t max_chunks,
                    hipStream_t s) {
     if constexpr (!std::is_same<E, F32>::value && (kD == 64 || kD == 128)) {
-        if (p.block_size.divisor == 16 && rows <= kPlanRows && p.width > 0) {
+        // The kernel counts work items in 32 bits (at most 512-token chunks);
+        // rows <= kPlanRows keeps the product below 2^51.
+        if (p.block_size.divisor == 16 && rows <= kPlanRows && p.width > 0 &&
+            rows * max_chunks * p.heads <= 0xffffffffULL) {
             switch (group) {
             case 1: return launch_bs16<E, kD, 1>(p, max_chunks, s);
             case 2: return launch_bs16<E, kD, 2>(p, max_chunks, s);
