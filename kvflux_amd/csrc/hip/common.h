@@ -88,6 +88,30 @@ __device__ inline void stream_store(Vec* p, const Vec& v) {
     }
 }
 
+// An empty asm that reads v: the loads filling a thread's registers must all
+// be complete here, and the compiler cannot sink a load into the branch that
+// stores its value. Used between a thread's (unconditional) loads and its
+// conditional stores: with loads inside the branches the compiler's wait
+// counts turn conservative and every store waits for the previous store
+// (vmcnt counts stores on gfx9), which serialises them.
+template <typename Vec>
+__device__ inline void keep_in_registers(const Vec& v) {
+    if constexpr (sizeof(Vec) == 16) {
+        typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+        asm volatile("" ::"v"(__builtin_bit_cast(u32x4_t, v)));
+    } else if constexpr (sizeof(Vec) == 8) {
+        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+        asm volatile("" ::"v"(__builtin_bit_cast(u32x2_t, v)));
+    } else if constexpr (sizeof(Vec) == 4) {
+        asm volatile("" ::"v"(__builtin_bit_cast(std::uint32_t, v)));
+    } else {
+        static_assert(sizeof(Vec) < 4, "raw vectors of 1, 2, 4, 8 or 16 bytes");
+        std::uint32_t w = 0;
+        __builtin_memcpy(&w, &v, sizeof(Vec));
+        asm volatile("" ::"v"(w));
+    }
+}
+
 // Widest power-of-two byte width (<= 16) that divides `row_bytes` and every
 // address in `ptrs`.
 inline unsigned copy_width(std::uint64_t row_bytes, const void* const* ptrs, int n) {

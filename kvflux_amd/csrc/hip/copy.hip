@@ -7,8 +7,9 @@
 // layout K/V[num_blocks][H][bs][D]). Raw bit copy.
 //
 // gfx950 mapping: grid (pair, 16 KiB part of the page, K or V). A workgroup of
-// 512 threads moves its part with 16-byte loads, all issued before the
-// stores, so one wavefront streams 1 KiB contiguous per instruction. The pair
+// 512 threads moves its part with 16-byte loads, all issued (unconditionally)
+// before the stores, which then go out back to back, so one wavefront
+// streams 1 KiB contiguous per instruction. The pair
 // is read once per workgroup (uniform, scalar loads).
 //
 // The same part copy moves KV chunks between the GPU and pinned host memory
@@ -34,8 +35,10 @@ __device__ inline void copy_part(const Vec* __restrict__ from, Vec* __restrict__
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
         const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
-        if (i < n) r[u] = stream_load(from + i);
+        r[u] = stream_load(from + (i < n ? i : 0));  // n >= 1: vector 0 is in range
     }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) keep_in_registers(r[u]);
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
         const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
@@ -92,8 +95,10 @@ __global__ __launch_bounds__(kCopyThreads) void copy_chunks_kernel(const std::ui
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
             const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
-            if (i < n) r[u] = from[i];
+            r[u] = from[i < n ? i : 0];  // n >= 1: vector 0 is in range
         }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) keep_in_registers(r[u]);
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
             const std::uint64_t i = first + static_cast<std::uint64_t>(u) * kCopyThreads;
