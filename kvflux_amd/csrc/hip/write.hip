@@ -13,7 +13,10 @@
 // independent slot and row loads in flight than fewer threads moving several
 // vectors each. Measured on MI355X for 4096 tokens x 8 heads x 128 BF16
 // (33.6 MB): 1024-thread workgroups 5.3 us on two boxes, 512 5.3-5.55 us,
-// 256 5.65 us; two vectors per thread 17.5 us at every workgroup size.
+// 256 5.65 us; two vectors per thread 17.5 us at every workgroup size (their
+// loads sat under per-vector branches, each branch waiting for its own).
+// The K/V loads are issued with the slot load instead of after it:
+// 5.14 against 5.46 us (median of five).
 #include "common.h"
 
 namespace kvflux_hip {
@@ -55,26 +58,33 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel(
     Vec k[kUnroll], v[kUnroll];
     std::uint64_t dst[kUnroll];
     bool live[kUnroll];
+    // The row loads do not depend on the slot: they are issued unconditionally
+    // (a thread past the end rereads vector 0) together with the slot load,
+    // so a thread waits for one memory round trip, not two (a load under the
+    // slot test is issued only after the slot has arrived).
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-        const std::uint32_t i = first + u * kThreads;
-        live[u] = i < total_vectors;
-        dst[u] = 0;
-        if (live[u]) {
-            const std::uint32_t row = vectors_per_row.div(i);
-            const std::uint32_t col = i - row * vectors_per_row.divisor;
-            const std::uint32_t token = heads.div(row);
-            const std::uint32_t head = row - token * heads.divisor;
-            const std::uint64_t slot = slot_of(token);
-            live[u] = slot < slot_count;  // never write outside the arena
-            const std::uint32_t s = static_cast<std::uint32_t>(slot);
-            const std::uint32_t page = block_size.div(s);
-            const std::uint32_t offset = s - page * block_size.divisor;
-            dst[u] = ((static_cast<std::uint64_t>(page) * heads.divisor + head) *
-                          block_size.divisor + offset) * vectors_per_row.divisor + col;
-            k[u] = key_new[i];
-            v[u] = value_new[i];
-        }
+        const std::uint32_t i0 = first + u * kThreads;
+        const bool in_range = i0 < total_vectors;
+        const std::uint32_t i = in_range ? i0 : 0u;  // total_vectors >= 1
+        k[u] = key_new[i];
+        v[u] = value_new[i];
+        const std::uint32_t row = vectors_per_row.div(i);
+        const std::uint32_t col = i - row * vectors_per_row.divisor;
+        const std::uint32_t token = heads.div(row);
+        const std::uint32_t head = row - token * heads.divisor;
+        const std::uint64_t slot = slot_of(token);
+        live[u] = in_range && slot < slot_count;  // never write outside the arena
+        const std::uint32_t s = static_cast<std::uint32_t>(slot);
+        const std::uint32_t page = block_size.div(s);
+        const std::uint32_t offset = s - page * block_size.divisor;
+        dst[u] = ((static_cast<std::uint64_t>(page) * heads.divisor + head) *
+                      block_size.divisor + offset) * vectors_per_row.divisor + col;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        keep_in_registers(k[u]);
+        keep_in_registers(v[u]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -96,15 +106,19 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel_wide(
     const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
     for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
          i < total_vectors; i += stride) {
+        const Vec k = key_new[i];
+        const Vec v = value_new[i];
         const std::uint64_t row = i / vectors_per_row, col = i % vectors_per_row;
         const std::uint64_t token = row / heads, head = row % heads;
         const std::uint64_t slot = slot_of(token);
+        keep_in_registers(k);
+        keep_in_registers(v);
         if (slot >= slot_count) continue;
         const std::uint64_t d =
             ((slot / block_size * heads + head) * block_size + slot % block_size) *
                 vectors_per_row + col;
-        key_cache[d] = key_new[i];
-        value_cache[d] = value_new[i];
+        key_cache[d] = k;
+        value_cache[d] = v;
     }
 }
 
