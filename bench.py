@@ -27,7 +27,8 @@ Also measured in the same run (sub-objects of the JSON line):
            same rows on all cores of the process's CPU share (at most 16) in
            `all_cores`, and the CPU model.
   write, gather and prefill also report the synchronous C++ API time
-  (`api_us` / `api_ms`: validation, metadata upload, launch, synchronisation).
+  (`api_us` / `api_ms`: validation, metadata upload, launch, synchronisation),
+  timed in C++ by the extension's `timing` module.
 
 roofline.traffic is the HBM traffic of one decode call measured with
 rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by what the same counters read
@@ -424,11 +425,9 @@ def bench_write(v2, args, stream):
     slot_list = slots.tolist()
     for _ in range(3):
         v2.write_paged_kv(storage, kn.ptr, vn.ptr, slot_list)
-    t0 = time.perf_counter()
-    reps = 20
-    for _ in range(reps):
-        v2.write_paged_kv(storage, kn.ptr, vn.ptr, slot_list)
-    api_us = (time.perf_counter() - t0) / reps * 1e6
+    # The synchronous C++ API, timed in C++ (the Python binding would add the
+    # conversion of 4096 slots from a Python list to every call).
+    api_us = v2.timing.write_paged_kv(storage, kn.ptr, vn.ptr, slot_list, 50) * 1e6
 
     # Bit-exact check of every touched page (and its untouched slots).
     page_elems = H * bs * D
@@ -494,11 +493,7 @@ def bench_gather(v2, args, stream, dtype_name: str):
     # The synchronous C++ API on the same batch (validation, metadata upload,
     # one launch, stream synchronisation).
     v2.read_paged_kv_batch(storage, seqs, ko.ptr, vo.ptr)
-    reps = 10
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        v2.read_paged_kv_batch(storage, seqs, ko.ptr, vo.ptr)
-    api_us = (time.perf_counter() - t0) / reps * 1e6
+    api_us = v2.timing.read_paged_kv_batch(storage, seqs, ko.ptr, vo.ptr, 10) * 1e6
     # Bit-exact check of a few sequences against the oracle gather.
     page_elems = H * bs * D
     mism = 0
@@ -557,13 +552,9 @@ def bench_prefill(v2, args, stream):
     ms = time_launches(launch, stream, max(1, args.warmup // 2), max(3, args.steps // 4))
     # The synchronous C++ API (paged_attention with AttentionPrecision::Fast,
     # one call per sequence) on the same inputs.
-    reps = 3
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        for i in range(S):
-            v2.paged_attention(storage, seqs[i], qs[i].ptr, out.ptr + i * T * Hq * D * 4, T, Hq,
-                               v2.AttentionPrecision.Fast)
-    api_ms = (time.perf_counter() - t0) / reps * 1e3
+    api_ms = v2.timing.paged_attention(storage, seqs, [qs[i].ptr for i in range(S)],
+                                       [out.ptr + i * T * Hq * D * 4 for i in range(S)], Hq,
+                                       v2.AttentionPrecision.Fast, 3) * 1e3
     flops = S * T * (T + 1) / 2 * Hq * D * 4
     # The last queries (longest rows) of the first and last sequence against the CPU reference.
     page_bytes = H * bs * D * 2

@@ -65,6 +65,11 @@ public:
     void release(BlockHandle handle);
     std::size_t ref_count(BlockHandle handle) const;
     bool is_published(BlockHandle handle) const;
+    // Page ids of n handles that each hold a reference, checked as
+    // ref_count does (std::invalid_argument for a stale handle, or one with no
+    // reference); out[i] = handles[i].id. One pass, for building tables.
+    // No counterpart in the reference.
+    void referenced_ids(const BlockHandle* handles, std::size_t n, std::size_t* out) const;
 
     // Index a privately held full block under the tokens from the start of
     // the sequence to the end of that block.

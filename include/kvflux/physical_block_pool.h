@@ -35,6 +35,9 @@ public:
 
     // Page id of a live handle; std::invalid_argument for stale handles.
     PhysicalBlockID id(PhysicalBlockHandle handle) const;
+    // id() of n handles at once (same checks and exceptions), into out[0..n).
+    // No counterpart in the reference.
+    void ids(const PhysicalBlockHandle* handles, std::size_t n, PhysicalBlockID* out) const;
     std::size_t ref_count(PhysicalBlockHandle handle) const;
     std::size_t capacity() const noexcept;
     std::size_t block_size() const noexcept;

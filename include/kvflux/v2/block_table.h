@@ -29,6 +29,9 @@ public:
     void append_shared(const BlockTable& source, std::size_t logical_block);
 
     PhysicalBlockID physical_id(std::size_t logical_block) const;
+    // physical_id of every entry, in order, into out[0..size()). No
+    // counterpart in the reference.
+    void physical_ids(PhysicalBlockID* out) const;
     PhysicalBlockHandle handle(std::size_t logical_block) const;
     std::size_t ref_count(std::size_t logical_block) const;
     PhysicalBlockID operator[](std::size_t logical_block) const {

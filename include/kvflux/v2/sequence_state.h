@@ -52,6 +52,9 @@ public:
     TokenLocation append_token_with_copy(const BlockCopier& copy);
 
     PhysicalBlockID physical_block_id(std::size_t logical_block) const;
+    // physical_block_id of every allocated block, in order, into
+    // out[0..num_allocated_blocks()). No counterpart in the reference.
+    void physical_block_ids(PhysicalBlockID* out) const;
     TokenLocation token_location(std::size_t token_index) const;
 
 private:

@@ -22,6 +22,7 @@
 #include "kvflux/v3/gpu_cpu_transfer.h"
 #include "kvflux/v3/pinned_chunk_pool.h"
 
+#include <chrono>
 #include <cstdint>
 #include <stdexcept>
 
@@ -42,6 +43,47 @@ void* ptr(std::uintptr_t address) { return reinterpret_cast<void*>(address); }
 std::uintptr_t addr(const void* p) { return reinterpret_cast<std::uintptr_t>(p); }
 
 } // namespace
+
+// Seconds per call of `fn` over `reps` back-to-back calls, timed in C++ (no
+// Python or argument conversion inside the timed loop).
+template <typename Fn>
+static double seconds_per_call(std::size_t reps, Fn&& fn) {
+    if (reps == 0) throw std::invalid_argument("reps must be positive");
+    const auto t0 = std::chrono::steady_clock::now();
+    for (std::size_t i = 0; i < reps; ++i) fn();
+    const std::chrono::duration<double> dt = std::chrono::steady_clock::now() - t0;
+    return dt.count() / static_cast<double>(reps);
+}
+
+// Timing loops over the synchronous C++ API, for the benchmark: what a C++
+// caller of the drop-in API pays per call (validation, metadata upload,
+// launch, stream synchronisation).
+static void bind_timing(py::module_ t) {
+    t.def("write_paged_kv", [](PagedKVStorage& s, std::uintptr_t k, std::uintptr_t v, const SlotMapping& slots,
+                               std::size_t reps) {
+        py::gil_scoped_release release;
+        return seconds_per_call(reps, [&] { write_paged_kv(s, ptr(k), ptr(v), slots); });
+    });
+    t.def("read_paged_kv_batch", [](const PagedKVStorage& s, const std::vector<const SequenceState*>& seqs,
+                                    std::uintptr_t k, std::uintptr_t v, std::size_t reps) {
+        py::gil_scoped_release release;
+        return seconds_per_call(reps, [&] { read_paged_kv_batch(s, seqs, ptr(k), ptr(v)); });
+    });
+    t.def("paged_attention", [](const PagedKVStorage& s, const std::vector<const SequenceState*>& seqs,
+                                const std::vector<std::uintptr_t>& q, const std::vector<std::uintptr_t>& o,
+                                std::size_t query_heads, AttentionPrecision precision, std::size_t reps) {
+        if (q.size() != seqs.size() || o.size() != seqs.size()) {
+            throw std::invalid_argument("one query and one output buffer per sequence");
+        }
+        py::gil_scoped_release release;
+        return seconds_per_call(reps, [&] {
+            for (std::size_t i = 0; i < seqs.size(); ++i) {
+                paged_attention(s, *seqs[i], static_cast<const float*>(ptr(q[i])), static_cast<float*>(ptr(o[i])),
+                                seqs[i]->num_tokens(), query_heads, precision);
+            }
+        });
+    }, "all sequences' tokens as queries (whole-prompt prefill), one call per sequence");
+}
 
 static void bind_v3(py::module_ v3m) {
     namespace v3 = kvflux::v3;
@@ -416,6 +458,7 @@ PYBIND11_MODULE(_kvflux, m) {
                               static_cast<float*>(ptr(o)), query_heads);
     });
     bind_v3(m.def_submodule("v3", "kvflux::v3 tiered cache: tiers, directory, GPU <-> CPU transfer"));
+    bind_timing(m.def_submodule("timing", "seconds per call of the synchronous C++ API, timed in C++"));
     m.def("paged_attention_batch", [](const PagedKVStorage& s, const DeviceBatchTable& t,
                                       std::uintptr_t q, std::uintptr_t o, std::size_t query_heads) {
         py::gil_scoped_release release;

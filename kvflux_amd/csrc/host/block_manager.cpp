@@ -94,6 +94,13 @@ void BlockManager::release(BlockHandle handle) {
 
 std::size_t BlockManager::ref_count(BlockHandle handle) const { return live(handle).refs; }
 
+void BlockManager::referenced_ids(const BlockHandle* handles, std::size_t n, std::size_t* out) const {
+    for (std::size_t i = 0; i < n; ++i) {
+        if (live(handles[i]).refs == 0) throw std::invalid_argument("physical block has no active reference");
+        out[i] = handles[i].id;
+    }
+}
+
 bool BlockManager::is_published(BlockHandle handle) const { return live(handle).published; }
 
 void BlockManager::publish(BlockHandle handle, const Tokens& prefix) {

@@ -40,6 +40,10 @@ bool PhysicalBlockPool::is_published(PhysicalBlockHandle handle) const {
     return manager_.is_published(handle);
 }
 
+void PhysicalBlockPool::ids(const PhysicalBlockHandle* handles, std::size_t n, PhysicalBlockID* out) const {
+    manager_.referenced_ids(handles, n, out);
+}
+
 PhysicalBlockID PhysicalBlockPool::id(PhysicalBlockHandle handle) const {
     // ref_count validates range, liveness and generation; an idle published
     // page (zero references) is not addressable either.
@@ -116,6 +120,10 @@ void BlockTable::append_shared(const BlockTable& source, std::size_t logical_blo
 
 PhysicalBlockID BlockTable::physical_id(std::size_t logical_block) const {
     return pool_->id(entries_.at(logical_block));
+}
+
+void BlockTable::physical_ids(PhysicalBlockID* out) const {
+    if (!entries_.empty()) pool_->ids(entries_.data(), entries_.size(), out);
 }
 
 PhysicalBlockHandle BlockTable::handle(std::size_t logical_block) const {
@@ -247,6 +255,8 @@ PhysicalBlockID SequenceState::physical_block_id(std::size_t logical_block) cons
     return table_.physical_id(logical_block);
 }
 
+void SequenceState::physical_block_ids(PhysicalBlockID* out) const { table_.physical_ids(out); }
+
 PhysicalBlockHandle SequenceState::block_handle(std::size_t logical_block) const {
     return table_.handle(logical_block);
 }
@@ -309,20 +319,15 @@ BatchBlockTable build_batch_block_table(const std::vector<const SequenceState*>&
     }
     out.table_.assign(sequences.size() * out.width_, BatchBlockTable::invalid_block());
     for (std::size_t r = 0; r < sequences.size(); ++r) {
-        auto* row = out.table_.data() + r * out.width_;
-        for (std::size_t b = 0; b < sequences[r]->num_allocated_blocks(); ++b) {
-            row[b] = sequences[r]->physical_block_id(b);
-        }
+        sequences[r]->physical_block_ids(out.table_.data() + r * out.width_);
     }
     return out;
 }
 
 ReadBlockTable build_read_block_table(const SequenceState& sequence) {
     ReadBlockTable ids;
-    ids.reserve(sequence.num_allocated_blocks());
-    for (std::size_t b = 0; b < sequence.num_allocated_blocks(); ++b) {
-        ids.push_back(sequence.physical_block_id(b));
-    }
+    ids.resize(sequence.num_allocated_blocks());
+    sequence.physical_block_ids(ids.data());
     return ids;
 }
 
