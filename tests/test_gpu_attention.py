@@ -69,6 +69,8 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("BFloat16", 2, 4, 256, [64, 900]),
     ("Float16", 3, 3, 128, [100, 513]),
     ("BFloat16", 4, 8, 64, [1, 2000]),
+    ("BFloat16", 1, 8, 128, [3, 511, 1100, 2049]),
+    ("Float16", 2, 16, 128, [17, 700, 1600]),
 ]
 
 
@@ -255,26 +257,28 @@ def test_shared_full_chunks_mixed_batch(gpu, v2, name, kv_heads, q_heads, head_s
     assert np.array_equal(od2.download(np.float32).view(np.uint32), got.view(np.uint32))
 
 
-ITEM_CASES = [  # name, head_size, rows, max_len
-    ("BFloat16", 128, 128, 16384),
-    ("Float16", 128, 128, 32768),
-    ("BFloat16", 128, 256, 32768),
-    ("BFloat16", 64, 256, 16384),
+ITEM_CASES = [  # name, head_size, rows, max_len, query heads (2 kv heads)
+    ("BFloat16", 128, 128, 16384, 8),
+    ("Float16", 128, 128, 32768, 8),
+    ("BFloat16", 128, 256, 32768, 8),
+    ("BFloat16", 64, 256, 16384, 8),
+    ("BFloat16", 128, 128, 32768, 16),
 ]
 
 
-@pytest.mark.parametrize("name,head_size,rows,max_len", ITEM_CASES)
-def test_decode_work_item_sizes(gpu, name, head_size, rows, max_len):
+@pytest.mark.parametrize("name,head_size,rows,max_len,q_heads", ITEM_CASES)
+def test_decode_work_item_sizes(gpu, name, head_size, rows, max_len, q_heads):
     """The block-size-16 decode kernel splits rows into work items of 512 to
     4096 tokens, the largest that leaves at least 8 items per resident
     workgroup for rows of max_len tokens. With 2 kv heads on a 256-CU MI355X
     (512 resident workgroups at head_size 128, 768 at 64) these batches take
-    1024-, 2048-, 4096- and 1024-token items. Rows map onto a small page pool
+    1024-, 2048-, 4096- and 1024-token items (the GQA-group-8 case 2048).
+    Rows map onto a small page pool
     with repeats, so long rows need little memory; lengths sit on every item
     boundary (and 0). Sampled rows match the oracle at 1e-5, and two calls
     are bit-identical."""
     lib = capi.lib()
-    H, Hq, bs, P = 2, 8, 16, 4096
+    H, Hq, bs, P = 2, q_heads, 16, 4096
     code = DTYPES[name][0]
     esize = 2
     page = H * bs * head_size
