@@ -1232,7 +1232,11 @@ int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint6
             switch (group) {
             case 1: return launch_bs16<E, kD, 1>(p, max_chunks, s);
             case 2: return launch_bs16<E, kD, 2>(p, max_chunks, s);
+            case 3: return launch_bs16<E, kD, 3>(p, max_chunks, s);
             case 4: return launch_bs16<E, kD, 4>(p, max_chunks, s);
+            case 5: return launch_bs16<E, kD, 5>(p, max_chunks, s);
+            case 6: return launch_bs16<E, kD, 6>(p, max_chunks, s);
+            case 7: return launch_bs16<E, kD, 7>(p, max_chunks, s);
             case 8:
                 // 251 VGPRs at kD = 128 (no spills, two workgroups per CU):
                 // 1.27 against 3.10 ms on the VALU split kernel for 128 rows
@@ -1264,10 +1268,12 @@ int dispatch(Params p, std::uint64_t rows, std::uint64_t head_dim, std::uint64_t
     }
 }
 
+// Whether a call may write chunk partials (and so needs the workspace): the
+// block-size-16 kernel at head_size 64/128 with groups 1..8, and the split
+// kernel at head_size 64/128 (groups 1, 2, 4, 8) or 256 (groups 1, 2, 4).
 bool uses_split(std::uint64_t head_dim, std::uint64_t group) {
-    const bool g_ok = group == 1 || group == 2 || group == 4 || group == 8;
-    if (head_dim == 64 || head_dim == 128) return g_ok;
-    if (head_dim == 256) return g_ok && group <= 4;
+    if (head_dim == 64 || head_dim == 128) return group >= 1 && group <= 8;
+    if (head_dim == 256) return group == 1 || group == 2 || group == 4;
     return false;
 }
 

@@ -2,7 +2,7 @@
 
 The reference's own GPU tests (test_gpu_reference_mirror.py) use head sizes
 3 and 4, which run on the generic kernel; these cases cover the tuned
-split-K instantiations (head_size 64/128/256, GQA groups 1/2/4/8), rows
+split-K instantiations (head_size 64/128/256, GQA groups 1 to 8), rows
 shorter and longer than one 512-token split, fragmented and shared pages,
 and the three cache dtypes, all at the 1e-5 bound of the reference's tests.
 """
@@ -71,6 +71,11 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("BFloat16", 4, 8, 64, [1, 2000]),
     ("BFloat16", 1, 8, 128, [3, 511, 1100, 2049]),
     ("Float16", 2, 16, 128, [17, 700, 1600]),
+    ("BFloat16", 2, 6, 128, [9, 600, 1500]),
+    ("Float16", 1, 5, 64, [4, 513, 1200]),
+    ("BFloat16", 2, 12, 64, [31, 1000]),
+    ("Float16", 1, 7, 128, [2, 777, 2100]),
+    ("BFloat16", 4, 28, 128, [100, 1300]),
 ]
 
 
