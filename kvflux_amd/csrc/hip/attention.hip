@@ -174,6 +174,11 @@ struct Params {
     std::uint32_t row_base;  // first row of this launch slice
     float scale_log2;        // log2(e) / sqrt(D)
     std::uint32_t chunk_shift;  // block-size-16 kernel: log2(tokens per work item), 9..12
+    // Block-size-16 kernel: query heads per kv head (the GQA group) and the
+    // first of them this launch serves (a group above 8 runs as several
+    // launches of a sub-group).
+    std::uint32_t q_group;
+    std::uint32_t q_first;
 };
 
 __device__ inline std::uint64_t row_length(const Params& p, std::uint32_t row) {
@@ -705,7 +710,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     };
     // Query elements tid + kThreads * i of the item's kG heads (clamped).
     auto fetch_query = [&](const Item& it, float (&q)[kQPer]) {
-        const float* base = p.query + (static_cast<std::uint64_t>(it.row) * p.query_heads + it.kvh * kG) * kD;
+        const float* base =
+            p.query + (static_cast<std::uint64_t>(it.row) * p.query_heads + it.kvh * p.q_group + p.q_first) * kD;
 #pragma unroll
         for (int i = 0; i < kQPer; ++i) {
             const int idx = tid + kThreads * i;
@@ -950,7 +956,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         __syncthreads();
 
         const bool single = lens[cur.row] <= chunk_tokens || p.max_chunks <= 1;
-        const std::uint32_t qh0 = cur.kvh * kG;
+        const std::uint32_t qh0 = cur.kvh * p.q_group + p.q_first;
         for (int idx = tid; idx < kG * kD; idx += kThreads) {
             const int g = idx / kD, d = idx % kD;
             float m = -INFINITY;
@@ -1173,7 +1179,7 @@ int launch_generic(Params p, std::uint64_t rows, std::uint64_t head_dim, hipStre
 
 // Persistent grid: every resident workgroup slot gets one workgroup.
 template <typename E, int kD, int kG>
-int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s) {
+int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s, bool combine) {
     static int slots = 0;  // resident workgroups per device (queried once)
     if (slots == 0) {
         int device = 0, cus = 0, per_cu = 0;
@@ -1206,7 +1212,7 @@ int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s) {
     hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG>), dim3(grid), dim3(kThreads), 0, s, p);
     int status = launch_status("paged_decode_bs16_kernel");
     if (status != KVFLUX_OK) return status;
-    if (max_chunks > 1) {
+    if (combine && max_chunks > 1) {
         for (std::uint64_t base = 0; base < p.num_rows; base += 0x7fffffffULL / p.query_heads) {
             const std::uint64_t n = p.num_rows - base < 0x7fffffffULL / p.query_heads
                                         ? p.num_rows - base : 0x7fffffffULL / p.query_heads;
@@ -1229,21 +1235,34 @@ int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint6
         // rows <= kPlanRows keeps the product below 2^51.
         if (p.block_size.divisor == 16 && rows <= kPlanRows && p.width > 0 &&
             rows * max_chunks * p.heads <= 0xffffffffULL) {
-            switch (group) {
-            case 1: return launch_bs16<E, kD, 1>(p, max_chunks, s);
-            case 2: return launch_bs16<E, kD, 2>(p, max_chunks, s);
-            case 3: return launch_bs16<E, kD, 3>(p, max_chunks, s);
-            case 4: return launch_bs16<E, kD, 4>(p, max_chunks, s);
-            case 5: return launch_bs16<E, kD, 5>(p, max_chunks, s);
-            case 6: return launch_bs16<E, kD, 6>(p, max_chunks, s);
-            case 7: return launch_bs16<E, kD, 7>(p, max_chunks, s);
-            case 8:
-                // 251 VGPRs at kD = 128 (no spills, two workgroups per CU):
-                // 1.27 against 3.10 ms on the VALU split kernel for 128 rows
-                // of U[1024, 32768] tokens with 64 query / 8 kv heads.
-                return launch_bs16<E, kD, 8>(p, max_chunks, s);
-            default: break;
+            // A group above 8 runs as launches of a sub-group: the largest
+            // divisor of the group up to 8, each launch serving its slice of
+            // the query heads (and reading K/V again); the chunk partials of
+            // all of them are combined once, after the last. Group 8 at
+            // kD = 128 takes 251 VGPRs (no spills, two workgroups per CU):
+            // 1.27 against 3.10 ms on the VALU split kernel for 128 rows of
+            // U[1024, 32768] tokens with 64 query / 8 kv heads.
+            const auto g = static_cast<std::uint32_t>(group);
+            std::uint32_t sub = g < 8 ? g : 8;
+            while (g % sub != 0) --sub;
+            p.q_group = g;
+            for (std::uint32_t first = 0; first < g; first += sub) {
+                p.q_first = first;
+                const bool last = first + sub >= g;
+                int status = KVFLUX_OK;
+                switch (sub) {
+                case 1: status = launch_bs16<E, kD, 1>(p, max_chunks, s, last); break;
+                case 2: status = launch_bs16<E, kD, 2>(p, max_chunks, s, last); break;
+                case 3: status = launch_bs16<E, kD, 3>(p, max_chunks, s, last); break;
+                case 4: status = launch_bs16<E, kD, 4>(p, max_chunks, s, last); break;
+                case 5: status = launch_bs16<E, kD, 5>(p, max_chunks, s, last); break;
+                case 6: status = launch_bs16<E, kD, 6>(p, max_chunks, s, last); break;
+                case 7: status = launch_bs16<E, kD, 7>(p, max_chunks, s, last); break;
+                default: status = launch_bs16<E, kD, 8>(p, max_chunks, s, last); break;
+                }
+                if (status != KVFLUX_OK) return status;
             }
+            return KVFLUX_OK;
         }
     }
     switch (group) {
@@ -1269,10 +1288,10 @@ int dispatch(Params p, std::uint64_t rows, std::uint64_t head_dim, std::uint64_t
 }
 
 // Whether a call may write chunk partials (and so needs the workspace): the
-// block-size-16 kernel at head_size 64/128 with groups 1..8, and the split
+// block-size-16 kernel at head_size 64/128 with any group, and the split
 // kernel at head_size 64/128 (groups 1, 2, 4, 8) or 256 (groups 1, 2, 4).
 bool uses_split(std::uint64_t head_dim, std::uint64_t group) {
-    if (head_dim == 64 || head_dim == 128) return group >= 1 && group <= 8;
+    if (head_dim == 64 || head_dim == 128) return group >= 1;
     if (head_dim == 256) return group == 1 || group == 2 || group == 4;
     return false;
 }
@@ -1358,6 +1377,8 @@ extern "C" int kvflux_paged_attention(const void* key_cache, const void* value_c
     p.query = query;
     p.output = output;
     p.max_chunks = static_cast<std::uint32_t>(chunks);
+    p.q_group = static_cast<std::uint32_t>(group);
+    p.q_first = 0;
     p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_size)));
     if (need > 0) {
         const std::uint64_t acc = num_rows * query_heads * chunks * head_size * sizeof(float);

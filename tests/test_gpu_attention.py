@@ -2,9 +2,10 @@
 
 The reference's own GPU tests (test_gpu_reference_mirror.py) use head sizes
 3 and 4, which run on the generic kernel; these cases cover the tuned
-split-K instantiations (head_size 64/128/256, GQA groups 1 to 8), rows
-shorter and longer than one 512-token split, fragmented and shared pages,
-and the three cache dtypes, all at the 1e-5 bound of the reference's tests.
+split-K instantiations (head_size 64/128/256; GQA groups 1 to 8, and groups
+above 8 as several launches of a sub-group), rows shorter and longer than
+one split, fragmented and shared pages, and the three cache dtypes, all at
+the 1e-5 bound of the reference's tests.
 """
 from __future__ import annotations
 
@@ -76,6 +77,10 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("BFloat16", 2, 12, 64, [31, 1000]),
     ("Float16", 1, 7, 128, [2, 777, 2100]),
     ("BFloat16", 4, 28, 128, [100, 1300]),
+    ("BFloat16", 2, 32, 128, [15, 640, 1700]),
+    ("Float16", 1, 12, 64, [5, 1030]),
+    ("BFloat16", 2, 20, 128, [300, 1111]),
+    ("BFloat16", 1, 11, 64, [1, 900]),
 ]
 
 
@@ -268,6 +273,7 @@ ITEM_CASES = [  # name, head_size, rows, max_len, query heads (2 kv heads)
     ("BFloat16", 128, 256, 32768, 8),
     ("BFloat16", 64, 256, 16384, 8),
     ("BFloat16", 128, 128, 32768, 16),
+    ("BFloat16", 128, 64, 32768, 32),
 ]
 
 
