@@ -179,6 +179,9 @@ struct Params {
     // launches of a sub-group).
     std::uint32_t q_group;
     std::uint32_t q_first;
+    // Block-size-16 kernel: log2(block_size / 16) (pages of 16 to 128
+    // tokens are cut into 16-token tiles).
+    std::uint32_t page_tiles_shift;
 };
 
 __device__ inline std::uint64_t row_length(const Params& p, std::uint32_t row) {
@@ -510,7 +513,7 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 }
 
 // ---------------------------------------------------------------- block_size 16 decode
-// Hot path for 16-token pages, 16-bit caches, head_size 64/128:
+// Hot path for pages of 16 (to 128) tokens, 16-bit caches, head_size 64/128:
 //  * persistent workgroups walk a plan of (row, chunk, kv head) items built
 //    in LDS from the row lengths (exclusive prefix of chunk counts), so no
 //    workgroup is launched for an empty chunk and consecutive items read the
@@ -519,9 +522,11 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 //    persistent grid): fewer, longer items mean fewer item epilogues and
 //    fewer chunk partials (4096 against 512 tokens: 1.227 against 1.37 ms
 //    for 128 rows of U[1024, 32768] tokens on MI355X);
-//  * a 16-token tile is exactly one page: its id is one uniform LDS read and
-//    every K/V address is that page's base plus a constant lane offset, and
-//    both K and V of a tile arrive as fully coalesced 16-byte loads;
+//  * a 16-token tile is one page (or a contiguous 1/2, 1/4, 1/8 of one
+//    kv head's rows of a 32-, 64- or 128-token page): its base offset is one
+//    lane read and every K/V address is that base plus a constant lane
+//    offset, and both K and V of a tile arrive as fully coalesced 16-byte
+//    loads;
 //  * QK^T of a tile is kD/32 MFMA 16x16x32 ops on the raw 16-bit K rows
 //    against Q split into hi/mid/lo 16-bit parts (FP32-equivalent); two DPP
 //    row shifts add the parts;
@@ -653,7 +658,10 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
 
     const T* kc = static_cast<const T*>(p.key_cache);
     const T* vc = static_cast<const T*>(p.value_cache);
-    const std::uint64_t head_stride = static_cast<std::uint64_t>(kBs) * kD;
+    // A page holds 2^page_tiles_shift 16-token tiles of every kv head:
+    // tile t of a row is tile t % 2^shift of page t >> shift.
+    const std::uint32_t tile_shift = p.page_tiles_shift;
+    const std::uint64_t head_stride = static_cast<std::uint64_t>(kBs << tile_shift) * kD;
     const std::uint64_t page_stride = head_stride * p.heads;
     // K: lane (quad, col) loads token col, dims 8*quad + 32*kk .. +8.
     const std::uint32_t k_lane = col * kD + quad * 8;
@@ -704,9 +712,11 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     // wave + kWaves * j, or kNoPage.
     auto fetch_pages = [&](const Item& it) -> std::uint64_t {
         const std::uint64_t* table_row = p.table + (p.seq_lens ? it.row : 0) * p.width;
-        const std::uint64_t logical = static_cast<std::uint64_t>(it.chunk) * tiles + wave + kWaves * (lane & (per_wave - 1));
+        const std::uint64_t tile = static_cast<std::uint64_t>(it.chunk) * tiles + wave + kWaves * (lane & (per_wave - 1));
+        const std::uint64_t logical = tile >> tile_shift;
         const std::uint64_t id = table_row[logical < p.width ? logical : p.width - 1];
-        return logical < p.width && id < p.num_blocks ? id * page_stride : kNoPage;
+        const std::uint64_t in_page = (tile & ((1u << tile_shift) - 1)) * (kBs * kD);
+        return logical < p.width && id < p.num_blocks ? id * page_stride + in_page : kNoPage;
     };
     // Query elements tid + kThreads * i of the item's kG heads (clamped).
     auto fetch_query = [&](const Item& it, float (&q)[kQPer]) {
@@ -1233,7 +1243,8 @@ int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint6
     if constexpr (!std::is_same<E, F32>::value && (kD == 64 || kD == 128)) {
         // The kernel counts work items in 32 bits (at most 512-token chunks);
         // rows <= kPlanRows keeps the product below 2^51.
-        if (p.block_size.divisor == 16 && rows <= kPlanRows && p.width > 0 &&
+        const std::uint32_t bs = p.block_size.divisor;
+        if ((bs == 16 || bs == 32 || bs == 64 || bs == 128) && rows <= kPlanRows && p.width > 0 &&
             rows * max_chunks * p.heads <= 0xffffffffULL) {
             // A group above 8 runs as launches of a sub-group: the largest
             // divisor of the group up to 8, each launch serving its slice of
@@ -1242,6 +1253,7 @@ int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint6
             // kD = 128 takes 251 VGPRs (no spills, two workgroups per CU):
             // 1.27 against 3.10 ms on the VALU split kernel for 128 rows of
             // U[1024, 32768] tokens with 64 query / 8 kv heads.
+            p.page_tiles_shift = bs == 16 ? 0u : bs == 32 ? 1u : bs == 64 ? 2u : 3u;
             const auto g = static_cast<std::uint32_t>(group);
             std::uint32_t sub = g < 8 ? g : 8;
             while (g % sub != 0) --sub;
