@@ -1,8 +1,10 @@
 // Causal paged prefill on MFMA (gfx950): BF16/FP16 caches, head_size 64/128.
 //
-// One workgroup (8 wavefronts, two per SIMD) owns one kv head and a block of 256 rows,
-// a row being a (query token, query head) pair of that kv head's group:
-// 256 / G tokens x G heads. Wavefront w owns row blocks 2w, 2w+1 of 16 rows
+// One workgroup (8 wavefronts, two per SIMD) owns one kv head and 16 row blocks
+// of 16 rows, a row being a (query token, query head) pair of G query heads of
+// that kv head: 16 * floor(16 / G) tokens x G heads (G = 1..8 or 16; the row
+// blocks past 16 / G * G idle when G does not divide 16; other GQA groups run
+// as passes over sub-groups of G heads). Wavefront w owns row blocks 2w, 2w+1
 // (row block b = head b % G, tokens 16 * (b / G) ..). Keys stream through
 // LDS in tiles of 64, double-buffered: K and V go from global memory straight
 // into LDS (global_load_lds_dwordx4, no staging registers and no LDS write
@@ -99,6 +101,8 @@ struct PrefillParams {
     std::uint32_t kv_len;
     std::uint32_t tq;         // query tokens (the last tq of kv_len)
     std::uint32_t query_heads;
+    std::uint32_t q_group;    // query heads per kv head
+    std::uint32_t q_first;    // first query head of the group this launch covers
     std::uint32_t qblocks;    // ceil(tq / tokens per workgroup)
     const float* query;       // [tq][query_heads][D]
     float* output;            // [tq][query_heads][D]
@@ -150,11 +154,11 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     constexpr int kRowBytes = kD * 2;
     constexpr int kTileBytes = kPfTile * kRowBytes;
     constexpr int kDma = kTileBytes / (kPfThreads * 16);  // tile loads per thread per cache
-    constexpr int kTok = kPfRows / kG;         // query tokens per workgroup
+    constexpr int kTok = 16 * (16 / kG);       // query tokens per workgroup
     constexpr int kVSwz = kCpr / 8;            // V slot swizzle multiplier
     constexpr float kLazy = 8.0f;
     static_assert(kDma >= 1 && kTileBytes % (kPfThreads * 16) == 0, "tile split");
-    static_assert(kPfRows % (16 * kG) == 0, "whole token blocks per workgroup");
+    static_assert(kG >= 1 && kG <= 16 && kPfRows == 16 * 16, "16 row blocks of 16 rows per workgroup");
 
     __shared__ __attribute__((aligned(16))) std::uint16_t ktile0[kPfTile * kD];
     __shared__ __attribute__((aligned(16))) std::uint16_t ktile1[kPfTile * kD];
@@ -187,7 +191,8 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         const std::uint32_t token = t0 + 16 * (b / kG) + col;
         row_token[n] = token;
         const std::uint32_t tq_safe = token < p.tq ? token : p.tq - 1;
-        const float* src = p.query + (static_cast<std::uint64_t>(tq_safe) * p.query_heads + kvh * kG + g) * kD;
+        const float* src =
+            p.query + (static_cast<std::uint64_t>(tq_safe) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
 #pragma unroll
         for (int kk = 0; kk < kSteps; ++kk) {
             const float4 lo = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8);
@@ -405,7 +410,8 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         const int g = b % kG;
         const std::uint32_t token = row_token[n];
         if (token < t_end) {
-            float* dst = p.output + (static_cast<std::uint64_t>(token) * p.query_heads + kvh * kG + g) * kD;
+            float* dst =
+                p.output + (static_cast<std::uint64_t>(token) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
                 *reinterpret_cast<float4*>(dst + 16 * dt + 4 * quad) =
@@ -415,19 +421,48 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     }
 }
 
+template <typename E, int kD, int kG>
+int launch_prefill_pass(const PrefillParams& p, hipStream_t s) {
+    PrefillParams q = p;
+    constexpr unsigned kTok = 16 * (16 / kG);
+    q.qblocks = (p.tq + kTok - 1) / kTok;
+    hipLaunchKernelGGL((paged_prefill_kernel<E, kD, kG>), dim3(q.qblocks * p.heads), dim3(kPfThreads), 0, s, q);
+    return launch_status("paged_prefill_kernel");
+}
+
+// Query heads per workgroup pass for a GQA group: the group itself up to 8
+// and at 16, else the largest divisor of it among 16, 8, 7, ..., 1 (then the
+// group runs as group / sub passes, each over every kv head).
+inline std::uint32_t prefill_sub_group(std::uint32_t group) {
+    if (group <= 8) return group;
+    if (group % 16 == 0) return 16;
+    for (std::uint32_t d = 8; d > 1; --d)
+        if (group % d == 0) return d;
+    return 1;
+}
+
 template <typename E, int kD>
 int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_t s) {
+    const std::uint32_t sub = prefill_sub_group(group);
     PrefillParams q = p;
-    const unsigned tok = kPfRows / group;
-    q.qblocks = (p.tq + tok - 1) / tok;
-    const dim3 grid(q.qblocks * p.heads);
-    switch (group) {
-    case 1: hipLaunchKernelGGL((paged_prefill_kernel<E, kD, 1>), grid, dim3(kPfThreads), 0, s, q); break;
-    case 2: hipLaunchKernelGGL((paged_prefill_kernel<E, kD, 2>), grid, dim3(kPfThreads), 0, s, q); break;
-    case 4: hipLaunchKernelGGL((paged_prefill_kernel<E, kD, 4>), grid, dim3(kPfThreads), 0, s, q); break;
-    default: hipLaunchKernelGGL((paged_prefill_kernel<E, kD, 8>), grid, dim3(kPfThreads), 0, s, q); break;
+    q.q_group = group;
+    for (std::uint32_t first = 0; first < group; first += sub) {
+        q.q_first = first;
+        int st = KVFLUX_OK;
+        switch (sub) {
+        case 1: st = launch_prefill_pass<E, kD, 1>(q, s); break;
+        case 2: st = launch_prefill_pass<E, kD, 2>(q, s); break;
+        case 3: st = launch_prefill_pass<E, kD, 3>(q, s); break;
+        case 4: st = launch_prefill_pass<E, kD, 4>(q, s); break;
+        case 5: st = launch_prefill_pass<E, kD, 5>(q, s); break;
+        case 6: st = launch_prefill_pass<E, kD, 6>(q, s); break;
+        case 7: st = launch_prefill_pass<E, kD, 7>(q, s); break;
+        case 8: st = launch_prefill_pass<E, kD, 8>(q, s); break;
+        default: st = launch_prefill_pass<E, kD, 16>(q, s); break;
+        }
+        if (st != KVFLUX_OK) return st;
     }
-    return launch_status("paged_prefill_kernel");
+    return KVFLUX_OK;
 }
 
 } // namespace
@@ -455,8 +490,7 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
     }
     const std::uint64_t group = query_heads / num_kv_heads;
     if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128) || !is_pow2(block_size) ||
-        block_size > 64 || (group != 1 && group != 2 && group != 4 && group != 8) ||
-        num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0xffffffffULL ||
+        block_size > 64 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0xffffffffULL ||
         query_heads > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
     }

@@ -85,6 +85,18 @@ CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("Float16", 2, 4, 64, 16, 600, 600),
     ("BFloat16", 4, 4, 64, 64, 300, 300),
     ("Float16", 1, 2, 128, 16, 513, 100),
+    # GQA groups that do not divide 16 row blocks (idle blocks per workgroup),
+    # group 16 (one token block per workgroup), and groups run as passes over
+    # sub-groups: 10 -> 2 x 5, 11 -> 11 x 1, 12 -> 2 x 6, 32 -> 2 x 16.
+    ("BFloat16", 2, 6, 128, 16, 500, 500),
+    ("Float16", 1, 5, 64, 32, 400, 170),
+    ("BFloat16", 2, 12, 64, 16, 300, 300),
+    ("BFloat16", 1, 7, 128, 16, 450, 450),
+    ("BFloat16", 2, 32, 128, 16, 260, 260),
+    ("BFloat16", 1, 10, 128, 16, 129, 40),
+    ("BFloat16", 1, 11, 64, 16, 150, 150),
+    ("Float16", 1, 12, 128, 64, 333, 333),
+    ("BFloat16", 1, 32, 64, 16, 200, 200),
 ]
 
 
