@@ -80,7 +80,8 @@ constexpr int kPfThreads = 512;   // 8 wavefronts, two per SIMD
 constexpr int kPfWaves = kPfThreads / 64;
 constexpr int kPfNt = 2;          // 16-row blocks per wavefront
 constexpr int kPfRows = kPfWaves * kPfNt * 16;  // rows per workgroup
-constexpr int kPfTile = 64;       // keys per LDS tile
+constexpr int kPfTileShift = 6;
+constexpr int kPfTile = 1 << kPfTileShift;  // keys per LDS tile
 constexpr int kPfTableMax = 2048; // page ids held in LDS (kv_len <= 2048 * block_size)
 // Flag bit of a missing page in the LDS page list (ids are below 2^31): its
 // K and V rows are loaded from pf_zero_rows instead.
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     const char* vc = static_cast<const char*>(p.value_cache);
     const std::uint32_t page_bytes = (static_cast<std::uint32_t>(kRowBytes) << p.bs_shift) * p.heads;
     const std::uint32_t head_bytes = (kvh << p.bs_shift) * kRowBytes;
-    const std::uint32_t tile_pages_shift = 6 - p.bs_shift;
+    const std::uint32_t tile_pages_shift = kPfTileShift - p.bs_shift;
     const std::uint32_t in_page_mask = (1u << p.bs_shift) - 1;
     auto kswz = [](int row) { return kCpr == 16 ? (row & 15) : ((row >> 1) & 7); };
     auto vswz = [](int row) { return kVSwz * (row & 7); };
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 
     auto compute_tile = [&](std::uint32_t tile, const std::uint16_t* kt, const std::uint16_t* vt) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < kPfTile / 32; ++h) {
             const std::uint32_t k0 = tile * kPfTile + 32 * h;
             if (k0 > last_key) break;  // uniform
             pf_f32x4_t s[2][kPfNt];
