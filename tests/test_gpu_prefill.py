@@ -143,24 +143,34 @@ def test_prefill_deterministic_and_unsupported(gpu):
                                     L + 1, Hq, qd.ptr, od.ptr, None) == capi.ERR_INVALID
 
 
-def test_prefill_through_cpp_layer(gpu, v2):
-    """AttentionPrecision::Fast routes a whole-prompt call to the MFMA kernel."""
+@pytest.mark.parametrize("kv_heads,q_heads", [(2, 8), (1, 16), (2, 10)])
+def test_prefill_through_cpp_layer(gpu, v2, kv_heads, q_heads):
+    """AttentionPrecision::Fast routes a whole-prompt call to the MFMA kernel
+    (GQA groups 4, 16 and 5)."""
     pool = v2.PhysicalBlockPool(64, 16)
-    storage = v2.PagedKVStorage(pool, 2, 128, v2.DType.BFloat16)
+    storage = v2.PagedKVStorage(pool, kv_heads, 128, v2.DType.BFloat16)
     seq = v2.SequenceState(1, pool)
     seq.append_tokens(500)
     n = storage.layout().cache_bytes() // 2
     device.fill_random(storage.key_base(), n, oracle.BF16, 1, 71)
     device.fill_random(storage.value_base(), n, oracle.BF16, 1, 72)
-    q = oracle.random_elements(0, 500 * 8 * 128, oracle.F32, 1, 73)
+    q = oracle.random_elements(0, 500 * q_heads * 128, oracle.F32, 1, 73)
     qd, od = buffer_like(q), buffer_like(np.zeros(q.size, np.float32))
-    v2.paged_attention(storage, seq, qd.ptr, od.ptr, 500, 8, v2.AttentionPrecision.Fast)
+    v2.paged_attention(storage, seq, qd.ptr, od.ptr, 500, q_heads, v2.AttentionPrecision.Fast)
     got = od.download(np.float32)
     kh = device.memcpy_d2h(storage.key_base(), storage.layout().cache_bytes(), np.uint16)
     vh = device.memcpy_d2h(storage.value_base(), storage.layout().cache_bytes(), np.uint16)
-    exp = oracle.paged_attention_causal(kh, vh, 2, 16, 128, oracle.BF16, v2.build_read_block_table(seq), 500, q,
-                                        500, 8, threads=8)
+    table = np.array(v2.build_read_block_table(seq), np.uint64)
+    exp = oracle.paged_attention_causal(kh, vh, kv_heads, 16, 128, oracle.BF16, table, 500, q, 500, q_heads,
+                                        threads=8)
     assert np.abs(got - exp).max() < 2e-2
+    # the same bits as the MFMA kernel called through the C ABI
+    td, od2 = buffer_like(table), buffer_like(np.zeros(q.size, np.float32))
+    assert capi.lib().kvflux_paged_prefill(storage.key_base(), storage.value_base(), 64, kv_heads, 16, 128,
+                                           capi.DTYPE_BF16, td.ptr, len(table), 500, 500, q_heads, qd.ptr,
+                                           od2.ptr, None) == 0
+    device.synchronize()
+    assert np.array_equal(od2.download(np.float32).view(np.uint32), got.view(np.uint32))
 
 
 GAP_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens, missing table entries
