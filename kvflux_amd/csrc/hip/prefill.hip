@@ -1,11 +1,12 @@
-// Causal paged prefill on MFMA (gfx950): BF16/FP16 caches, head_size 64/128.
+// Causal paged prefill on MFMA (gfx950): BF16/FP16 caches, head_size 64/128/256.
 //
-// One workgroup (8 wavefronts, two per SIMD) owns one kv head and 16 row blocks
-// of 16 rows, a row being a (query token, query head) pair of G query heads of
-// that kv head: 16 * floor(16 / G) tokens x G heads (G = 1..8 or 16; the row
-// blocks past 16 / G * G idle when G does not divide 16; other GQA groups run
-// as passes over sub-groups of G heads). Wavefront w owns row blocks 2w, 2w+1
-// (row block b = head b % G, tokens 16 * (b / G) ..). Keys stream through
+// One workgroup (8 wavefronts, two per SIMD) owns one kv head and R row blocks
+// of 16 rows (R = 16; 8 at head_size 256), a row being a (query token, query
+// head) pair of G query heads of that kv head: 16 * floor(R / G) tokens x G
+// heads (G <= 8, or 16 when R = 16; the row blocks past R / G * G idle when G
+// does not divide R; other GQA groups run as passes over sub-groups of G
+// heads). Wavefront w owns row blocks R/8 * w .. (row block b = head b % G,
+// tokens 16 * (b / G) ..). Keys stream through
 // LDS in tiles of 64, double-buffered: K and V go from global memory straight
 // into LDS (global_load_lds_dwordx4, no staging registers and no LDS write
 // instructions), the next tile's loads in flight while this tile is computed
@@ -78,17 +79,19 @@ __device__ inline float max_across_quads(float x) {
 
 constexpr int kPfThreads = 512;   // 8 wavefronts, two per SIMD
 constexpr int kPfWaves = kPfThreads / 64;
-constexpr int kPfNt = 2;          // 16-row blocks per wavefront
-constexpr int kPfRows = kPfWaves * kPfNt * 16;  // rows per workgroup
+// 16-row blocks per wavefront: two at head_size 64/128, one at 256 (whose
+// accumulators and Q operands take as many registers as two blocks at 128).
+template <int kD>
+constexpr int pf_blocks_per_wave() { return kD == 256 ? 1 : 2; }
 constexpr int kPfTileShift = 6;
 constexpr int kPfTile = 1 << kPfTileShift;  // keys per LDS tile
 constexpr int kPfTableMax = 2048; // page ids held in LDS (kv_len <= 2048 * block_size)
 // Flag bit of a missing page in the LDS page list (ids are below 2^31): its
 // K and V rows are loaded from pf_zero_rows instead.
 constexpr std::uint32_t kPfMissing = 0x80000000u;
-// One head's rows of one page at block_size <= 64 and head_size <= 128
+// One head's rows of one page at block_size <= 64 and head_size <= 256
 // (16-bit elements): the source of missing pages, all zeros.
-constexpr int kPfZeroBytes = 64 * 256;
+constexpr int kPfZeroBytes = 64 * 512;
 __device__ __attribute__((aligned(16))) unsigned char pf_zero_rows[kPfZeroBytes];
 
 struct PrefillParams {
@@ -155,11 +158,13 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     constexpr int kRowBytes = kD * 2;
     constexpr int kTileBytes = kPfTile * kRowBytes;
     constexpr int kDma = kTileBytes / (kPfThreads * 16);  // tile loads per thread per cache
-    constexpr int kTok = 16 * (16 / kG);       // query tokens per workgroup
+    constexpr int kPfNt = pf_blocks_per_wave<kD>();
+    constexpr int kBlocks = kPfWaves * kPfNt;   // 16-row blocks per workgroup
+    constexpr int kTok = 16 * (kBlocks / kG);  // query tokens per workgroup
     constexpr int kVSwz = kCpr / 8;            // V slot swizzle multiplier
     constexpr float kLazy = 8.0f;
     static_assert(kDma >= 1 && kTileBytes % (kPfThreads * 16) == 0, "tile split");
-    static_assert(kG >= 1 && kG <= 16 && kPfRows == 16 * 16, "16 row blocks of 16 rows per workgroup");
+    static_assert(kG >= 1 && kG <= kBlocks, "a row block per head of the group");
 
     __shared__ __attribute__((aligned(16))) std::uint16_t ktile0[kPfTile * kD];
     __shared__ __attribute__((aligned(16))) std::uint16_t ktile1[kPfTile * kD];
@@ -425,18 +430,19 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 template <typename E, int kD, int kG>
 int launch_prefill_pass(const PrefillParams& p, hipStream_t s) {
     PrefillParams q = p;
-    constexpr unsigned kTok = 16 * (16 / kG);
+    constexpr unsigned kTok = 16 * (kPfWaves * pf_blocks_per_wave<kD>() / kG);
     q.qblocks = (p.tq + kTok - 1) / kTok;
     hipLaunchKernelGGL((paged_prefill_kernel<E, kD, kG>), dim3(q.qblocks * p.heads), dim3(kPfThreads), 0, s, q);
     return launch_status("paged_prefill_kernel");
 }
 
-// Query heads per workgroup pass for a GQA group: the group itself up to 8
-// and at 16, else the largest divisor of it among 16, 8, 7, ..., 1 (then the
-// group runs as group / sub passes, each over every kv head).
-inline std::uint32_t prefill_sub_group(std::uint32_t group) {
+// Query heads per workgroup pass for a GQA group, with `blocks` row blocks
+// per workgroup (16, or 8 at head_size 256): the group itself up to 8 and at
+// 16 when blocks allow, else the largest divisor of it among 16, 8, 7, ..., 1
+// that fits (then the group runs as group / sub passes over every kv head).
+inline std::uint32_t prefill_sub_group(std::uint32_t group, std::uint32_t blocks) {
     if (group <= 8) return group;
-    if (group % 16 == 0) return 16;
+    if (blocks >= 16 && group % 16 == 0) return 16;
     for (std::uint32_t d = 8; d > 1; --d)
         if (group % d == 0) return d;
     return 1;
@@ -444,7 +450,8 @@ inline std::uint32_t prefill_sub_group(std::uint32_t group) {
 
 template <typename E, int kD>
 int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_t s) {
-    const std::uint32_t sub = prefill_sub_group(group);
+    constexpr int kBlocks = kPfWaves * pf_blocks_per_wave<kD>();
+    const std::uint32_t sub = prefill_sub_group(group, kBlocks);
     PrefillParams q = p;
     q.q_group = group;
     for (std::uint32_t first = 0; first < group; first += sub) {
@@ -459,11 +466,22 @@ int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_
         case 6: st = launch_prefill_pass<E, kD, 6>(q, s); break;
         case 7: st = launch_prefill_pass<E, kD, 7>(q, s); break;
         case 8: st = launch_prefill_pass<E, kD, 8>(q, s); break;
-        default: st = launch_prefill_pass<E, kD, 16>(q, s); break;
+        default:
+            if constexpr (kBlocks >= 16) st = launch_prefill_pass<E, kD, 16>(q, s);
+            break;
         }
         if (st != KVFLUX_OK) return st;
     }
     return KVFLUX_OK;
+}
+
+template <typename E>
+int launch_prefill_head_size(const PrefillParams& p, std::uint64_t head_size, std::uint32_t group, hipStream_t s) {
+    switch (head_size) {
+    case 64: return launch_prefill_group<E, 64>(p, group, s);
+    case 128: return launch_prefill_group<E, 128>(p, group, s);
+    default: return launch_prefill_group<E, 256>(p, group, s);
+    }
 }
 
 } // namespace
@@ -490,7 +508,7 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
         return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill: block table shorter than kv_len");
     }
     const std::uint64_t group = query_heads / num_kv_heads;
-    if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128) || !is_pow2(block_size) ||
+    if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128 && head_size != 256) || !is_pow2(block_size) ||
         block_size > 64 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0xffffffffULL ||
         query_heads > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
@@ -519,8 +537,6 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
     p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_size)));
     const hipStream_t s = as_stream(stream);
     const std::uint32_t g = static_cast<std::uint32_t>(group);
-    if (dtype == KVFLUX_DTYPE_BF16) {
-        return head_size == 64 ? launch_prefill_group<PfBf16, 64>(p, g, s) : launch_prefill_group<PfBf16, 128>(p, g, s);
-    }
-    return head_size == 64 ? launch_prefill_group<PfF16, 64>(p, g, s) : launch_prefill_group<PfF16, 128>(p, g, s);
+    if (dtype == KVFLUX_DTYPE_BF16) return launch_prefill_head_size<PfBf16>(p, head_size, g, s);
+    return launch_prefill_head_size<PfF16>(p, head_size, g, s);
 }

@@ -97,6 +97,12 @@ CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("BFloat16", 1, 11, 64, 16, 150, 150),
     ("Float16", 1, 12, 128, 64, 333, 333),
     ("BFloat16", 1, 32, 64, 16, 200, 200),
+    # head_size 256: 8 row blocks of 16 per workgroup (group 3 leaves 2 idle;
+    # group 16 runs as 2 x 8)
+    ("BFloat16", 2, 2, 256, 16, 400, 400),
+    ("Float16", 1, 3, 256, 32, 300, 120),
+    ("BFloat16", 2, 8, 256, 16, 260, 260),
+    ("BFloat16", 1, 16, 256, 64, 150, 150),
 ]
 
 
@@ -129,10 +135,12 @@ def test_prefill_deterministic_and_unsupported(gpu):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     lib = capi.lib()
     td, qd, od = buffer_like(table), buffer_like(q), buffer_like(np.zeros(q.size, np.float32))
-    # FP32 caches, head_size 96 and block_size 48 are left to the exact kernels.
+    # FP32 caches, head_sizes 96 and 512 and block_size 48 are left to the exact kernels.
     assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, bs, D, capi.DTYPE_F32, td.ptr, len(table), L, L,
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
     assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, bs, 96, capi.DTYPE_BF16, td.ptr, len(table), L, L,
+                                    Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
+    assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, bs, 512, capi.DTYPE_BF16, td.ptr, len(table), L, L,
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
     assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, 48, D, capi.DTYPE_BF16, td.ptr, len(table), L, L,
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
