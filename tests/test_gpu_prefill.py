@@ -181,6 +181,37 @@ def test_prefill_through_cpp_layer(gpu, v2, kv_heads, q_heads):
     assert np.array_equal(od2.download(np.float32).view(np.uint32), got.view(np.uint32))
 
 
+def test_precision_routing(gpu, v2):
+    """Auto sends calls of 16 or more query tokens to the MFMA prefill (the
+    same bits as Fast) and fewer to the exact kernels (the same bits as
+    Exact, which is within 1e-5 of the oracle)."""
+    pool = v2.PhysicalBlockPool(64, 16)
+    storage = v2.PagedKVStorage(pool, 2, 128, v2.DType.BFloat16)
+    seq = v2.SequenceState(1, pool)
+    seq.append_tokens(300)
+    n = storage.layout().cache_bytes() // 2
+    device.fill_random(storage.key_base(), n, oracle.BF16, 1, 81)
+    device.fill_random(storage.value_base(), n, oracle.BF16, 1, 82)
+    kh = device.memcpy_d2h(storage.key_base(), storage.layout().cache_bytes(), np.uint16)
+    vh = device.memcpy_d2h(storage.value_base(), storage.layout().cache_bytes(), np.uint16)
+    table = np.array(v2.build_read_block_table(seq), np.uint64)
+    P = v2.AttentionPrecision
+    for q_tokens in (15, 16):
+        q = oracle.random_elements(0, q_tokens * 8 * 128, oracle.F32, 1, 83 + q_tokens)
+        qd = buffer_like(q)
+        out = {}
+        for prec in (P.Auto, P.Fast, P.Exact):
+            od = buffer_like(np.zeros(q.size, np.float32))
+            v2.paged_attention(storage, seq, qd.ptr, od.ptr, q_tokens, 8, prec)
+            out[prec] = od.download(np.float32).view(np.uint32)
+        twin = P.Exact if q_tokens < 16 else P.Fast
+        assert np.array_equal(out[P.Auto], out[twin]), q_tokens
+        exp = oracle.paged_attention_causal(kh, vh, 2, 16, 128, oracle.BF16, table, 300, q, q_tokens, 8)
+        assert np.abs(out[P.Exact].view(np.float32) - exp).max() < 1e-5
+        assert np.abs(out[P.Fast].view(np.float32) - exp).max() < 2e-2
+    assert not np.array_equal(out[P.Fast], out[P.Exact])  # two different kernels
+
+
 GAP_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens, missing table entries
     ("BFloat16", 2, 8, 128, 4, 500, 500, [3, 40, 124]),
     ("Float16", 1, 8, 64, 8, 333, 120, [0, 20, 41]),
