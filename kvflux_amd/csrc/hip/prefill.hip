@@ -467,7 +467,11 @@ int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_
         case 7: st = launch_prefill_pass<E, kD, 7>(q, s); break;
         case 8: st = launch_prefill_pass<E, kD, 8>(q, s); break;
         default:
-            if constexpr (kBlocks >= 16) st = launch_prefill_pass<E, kD, 16>(q, s);
+            if constexpr (kBlocks >= 16) {
+                st = launch_prefill_pass<E, kD, 16>(q, s);
+            } else {
+                st = fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: sub-group %u", sub);
+            }
             break;
         }
         if (st != KVFLUX_OK) return st;
