@@ -85,7 +85,11 @@ template <int kD>
 constexpr int pf_blocks_per_wave() { return kD == 256 ? 1 : 2; }
 constexpr int kPfTileShift = 6;
 constexpr int kPfTile = 1 << kPfTileShift;  // keys per LDS tile
-constexpr int kPfTableMax = 2048; // page ids held in LDS (kv_len <= 2048 * block_size)
+// Page ids held in LDS per workgroup (kv_len <= that many pages): 8192
+// (32 KiB) beside the 64 KiB of tiles at head_size <= 128, 4096 beside the
+// 128 KiB at 256.
+template <int kD>
+constexpr int pf_table_max() { return kD == 256 ? 4096 : 8192; }
 // Flag bit of a missing page in the LDS page list (ids are below 2^31): its
 // K and V rows are loaded from pf_zero_rows instead.
 constexpr std::uint32_t kPfMissing = 0x80000000u;
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     __shared__ __attribute__((aligned(16))) std::uint16_t ktile1[kPfTile * kD];
     __shared__ __attribute__((aligned(16))) std::uint16_t vtile0[kPfTile * kD];
     __shared__ __attribute__((aligned(16))) std::uint16_t vtile1[kPfTile * kD];
-    __shared__ std::uint32_t pages[kPfTableMax];
+    __shared__ std::uint32_t pages[pf_table_max<kD>()];
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int col = lane % 16, quad = lane / 16;
@@ -517,11 +521,11 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
         query_heads > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
     }
+    const std::uint64_t table_max = head_size == 256 ? pf_table_max<256>() : pf_table_max<128>();
     const std::uint64_t pages_needed = (((kv_len + kPfTile - 1) / kPfTile) * kPfTile + block_size - 1) / block_size;
-    if (pages_needed > kPfTableMax) {
+    if (pages_needed > table_max) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: kv_len above %llu tokens",
-                    static_cast<unsigned long long>(kPfTableMax / ((kPfTile + block_size - 1) / block_size) *
-                                                    kPfTile));
+                    static_cast<unsigned long long>(table_max / ((kPfTile + block_size - 1) / block_size) * kPfTile));
     }
     PrefillParams p{};
     p.key_cache = key_cache;
@@ -532,7 +536,7 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
     while ((std::uint64_t{1} << shift) < block_size) ++shift;
     p.bs_shift = shift;
     p.table = block_table;
-    p.table_len = static_cast<std::uint32_t>(num_table_blocks < kPfTableMax ? num_table_blocks : kPfTableMax);
+    p.table_len = static_cast<std::uint32_t>(num_table_blocks < table_max ? num_table_blocks : table_max);
     p.kv_len = static_cast<std::uint32_t>(kv_len);
     p.tq = static_cast<std::uint32_t>(query_tokens);
     p.query_heads = static_cast<std::uint32_t>(query_heads);
