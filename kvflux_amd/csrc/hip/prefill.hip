@@ -85,9 +85,9 @@ template <int kD>
 constexpr int pf_blocks_per_wave() { return kD == 256 ? 1 : 2; }
 constexpr int kPfTileShift = 6;
 constexpr int kPfTile = 1 << kPfTileShift;  // keys per LDS tile
-// Page ids held in LDS per workgroup (kv_len <= that many pages): 8192
-// (32 KiB) beside the 64 KiB of tiles at head_size <= 128, 4096 beside the
-// 128 KiB at 256.
+// Page ids held in LDS per workgroup, one window of the sequence at a time:
+// 8192 (32 KiB) beside the 64 KiB of tiles at head_size <= 128, 4096 beside
+// the 128 KiB at 256.
 template <int kD>
 constexpr int pf_table_max() { return kD == 256 ? 4096 : 8192; }
 // Flag bit of a missing page in the LDS page list (ids are below 2^31): its
@@ -186,11 +186,21 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     const std::uint32_t last_key = past + t_end - 1;
     const std::uint32_t ntiles = last_key / kPfTile + 1;
     const std::uint32_t npages = ((ntiles * kPfTile - 1) >> p.bs_shift) + 1;
-    for (std::uint32_t i = tid; i < npages; i += kPfThreads) {
-        const std::uint64_t id = i < p.table_len ? p.table[i] : p.num_blocks;
-        const bool ok = id < p.num_blocks && (static_cast<std::uint64_t>(i) << p.bs_shift) < p.kv_len;
-        pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
-    }
+    const std::uint32_t tile_pages_shift = kPfTileShift - p.bs_shift;
+    // The page list holds a window of kWin pages (whole tiles) at a time: page
+    // `first` + i at pages[i]. A prompt longer than one window is restaged at
+    // each window boundary of the tile loop.
+    constexpr std::uint32_t kWin = pf_table_max<kD>();
+    const std::uint32_t win_mask = (kWin >> tile_pages_shift) - 1;  // tiles per window - 1
+    auto stage = [&](std::uint32_t first) {
+        for (std::uint32_t i = tid; i < kWin && first + i < npages; i += kPfThreads) {
+            const std::uint32_t pg = first + i;
+            const std::uint64_t id = pg < p.table_len ? p.table[pg] : p.num_blocks;
+            const bool ok = id < p.num_blocks && (static_cast<std::uint64_t>(pg) << p.bs_shift) < p.kv_len;
+            pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
+        }
+    };
+    stage(0);
 
     Vec qb_op[kPfNt][kSteps];
     std::uint32_t row_token[kPfNt];
@@ -225,7 +235,6 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     const char* vc = static_cast<const char*>(p.value_cache);
     const std::uint32_t page_bytes = (static_cast<std::uint32_t>(kRowBytes) << p.bs_shift) * p.heads;
     const std::uint32_t head_bytes = (kvh << p.bs_shift) * kRowBytes;
-    const std::uint32_t tile_pages_shift = kPfTileShift - p.bs_shift;
     const std::uint32_t in_page_mask = (1u << p.bs_shift) - 1;
     auto kswz = [](int row) { return kCpr == 16 ? (row & 15) : ((row >> 1) & 7); };
     auto vswz = [](int row) { return kVSwz * (row & 7); };
@@ -235,7 +244,8 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             const int e = (i * kPfWaves + wave) * 64 + lane;
             const int row = e / kCpr, slot = e % kCpr;
             const std::uint32_t r = static_cast<std::uint32_t>(row) & in_page_mask;
-            const std::uint32_t entry = pages[(tile << tile_pages_shift) + (static_cast<std::uint32_t>(row) >> p.bs_shift)];
+            const std::uint32_t entry =
+                pages[((tile & win_mask) << tile_pages_shift) + (static_cast<std::uint32_t>(row) >> p.bs_shift)];
             const std::uint32_t kchunk = (slot ^ kswz(row)) * 16, vchunk = (slot ^ vswz(row)) * 16;
             const char* ks;
             const char* vs;
@@ -383,9 +393,20 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     // tile's loads (2 * kDma per thread, issued one step earlier), then a
     // barrier publishes the tile; a second barrier frees the buffer.
     const bool tail = ntiles * kPfTile > p.kv_len;  // the last tile has keys past kv_len
+    // Called at the top of a step, before tile `next` is issued: every wave
+    // has issued (read the page list for) all tiles before it, behind the
+    // barrier that ended the previous step.
+    auto restage = [&](std::uint32_t next) {
+        if ((next & win_mask) == 0) {  // uniform
+            stage(next << tile_pages_shift);
+            wait_lgkm0();
+            lds_barrier();
+        }
+    };
     issue(0, std::integral_constant<int, 0>{});
     for (std::uint32_t tile = 0; tile < ntiles; tile += 2) {
         if (tile + 1 < ntiles) {
+            restage(tile + 1);
             issue(tile + 1, std::integral_constant<int, 1>{});
             wait_vm<2 * kDma>();
         } else {
@@ -399,6 +420,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         lds_barrier();
         if (tile + 1 >= ntiles) break;
         if (tile + 2 < ntiles) {
+            restage(tile + 2);
             issue(tile + 2, std::integral_constant<int, 0>{});
             wait_vm<2 * kDma>();
         } else {
@@ -517,16 +539,11 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
     }
     const std::uint64_t group = query_heads / num_kv_heads;
     if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128 && head_size != 256) || !is_pow2(block_size) ||
-        block_size > 64 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0xffffffffULL ||
+        block_size > 64 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0x7fffffffULL ||
         query_heads > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
     }
-    const std::uint64_t table_max = head_size == 256 ? pf_table_max<256>() : pf_table_max<128>();
-    const std::uint64_t pages_needed = (((kv_len + kPfTile - 1) / kPfTile) * kPfTile + block_size - 1) / block_size;
-    if (pages_needed > table_max) {
-        return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: kv_len above %llu tokens",
-                    static_cast<unsigned long long>(table_max / ((kPfTile + block_size - 1) / block_size) * kPfTile));
-    }
+
     PrefillParams p{};
     p.key_cache = key_cache;
     p.value_cache = value_cache;
@@ -536,7 +553,7 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
     while ((std::uint64_t{1} << shift) < block_size) ++shift;
     p.bs_shift = shift;
     p.table = block_table;
-    p.table_len = static_cast<std::uint32_t>(num_table_blocks < table_max ? num_table_blocks : table_max);
+    p.table_len = static_cast<std::uint32_t>(num_table_blocks < 0xffffffffULL ? num_table_blocks : 0xffffffffULL);
     p.kv_len = static_cast<std::uint32_t>(kv_len);
     p.tq = static_cast<std::uint32_t>(query_tokens);
     p.query_heads = static_cast<std::uint32_t>(query_heads);

@@ -103,10 +103,14 @@ CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("Float16", 1, 3, 256, 32, 300, 120),
     ("BFloat16", 2, 8, 256, 16, 260, 260),
     ("BFloat16", 1, 16, 256, 64, 150, 150),
-    # long prompts: more pages than 2048 in the workgroup's page list
+    # long prompts; the workgroup's page list holds 8192 pages (4096 at
+    # head_size 256) at a time and is restaged at each window boundary
     ("BFloat16", 2, 8, 128, 16, 40000, 64),
     ("Float16", 1, 2, 256, 16, 40000, 40),
     ("BFloat16", 1, 4, 64, 4, 30000, 33),
+    ("BFloat16", 1, 4, 64, 1, 20000, 300),
+    ("Float16", 1, 2, 256, 4, 40000, 40),
+    ("BFloat16", 2, 8, 128, 16, 140000, 16),
 ]
 
 
@@ -148,8 +152,8 @@ def test_prefill_deterministic_and_unsupported(gpu):
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
     assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, 48, D, capi.DTYPE_BF16, td.ptr, len(table), L, L,
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
-    # more pages than the workgroup's page list holds: 8192 at head_size 128
-    assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, 1, D, capi.DTYPE_BF16, td.ptr, 8256, 8193, 1,
+    # kv_len of 2^31 tokens or more (declined before anything is read)
+    assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, 1, D, capi.DTYPE_BF16, td.ptr, 2**31, 2**31, 1,
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
     # table too short for kv_len, more queries than tokens
     assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, bs, D, capi.DTYPE_BF16, td.ptr, 3, L, L,
