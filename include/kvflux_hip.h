@@ -177,6 +177,25 @@ int kvflux_paged_prefill(const void* key_cache, const void* value_cache,
                          uint64_t query_heads, const float* query, float* output,
                          void* stream);
 
+/* kvflux_paged_prefill_split: the same call with a device workspace, which
+ * lets the kernel split the key range of each (query block, kv head) over
+ * several workgroups when the call alone would not fill the GPU (a short
+ * query block against a long prefix, as in chunked prefill), merged by a
+ * second kernel. Same results within the bound (2e-2); same errors, plus
+ * KVFLUX_ERR_INVALID_ARGUMENT for a workspace smaller than
+ * kvflux_paged_prefill_workspace_size gives (0 bytes: no split is used, and
+ * the workspace may be NULL). No counterpart in the reference, whose
+ * paged_attention_kernel runs one thread per output element
+ * (src/v2/paged_attention.cu:108-128); the C++ paged_attention uses it. */
+int kvflux_paged_prefill_workspace_size(uint64_t num_kv_heads, uint64_t head_size, uint64_t kv_len,
+                                        uint64_t query_tokens, uint64_t query_heads, size_t* bytes);
+int kvflux_paged_prefill_split(const void* key_cache, const void* value_cache,
+                               uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
+                               uint64_t head_size, int dtype, const uint64_t* block_table,
+                               uint64_t num_table_blocks, uint64_t kv_len, uint64_t query_tokens,
+                               uint64_t query_heads, const float* query, float* output,
+                               void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Callers of the hot path: copy-on-write and device-side batch metadata.
  *

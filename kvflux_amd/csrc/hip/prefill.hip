@@ -115,6 +115,14 @@ struct PrefillParams {
     const float* query;       // [tq][query_heads][D]
     float* output;            // [tq][query_heads][D]
     float scale_log2;         // log2(e) / sqrt(D)
+    // Key splits: workgroup (split s) covers key tiles [s * split_tiles,
+    // (s + 1) * split_tiles). With splits > 1 it writes unnormalised partials
+    // (part_o [splits][tq][query_heads][D], part_ml [splits][tq][query_heads]
+    // {reference point, weight sum}) for paged_prefill_combine_kernel.
+    std::uint32_t splits;
+    std::uint32_t split_tiles;
+    float* part_o;
+    float* part_ml;
 };
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt(n) alone, lgkmcnt(0) alone.
@@ -179,12 +187,22 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int col = lane % 16, quad = lane / 16;
     const std::uint32_t kvh = blockIdx.x % p.heads;
-    const std::uint32_t qb = p.qblocks - 1 - blockIdx.x / p.heads;
+    const std::uint32_t split = (blockIdx.x / p.heads) % p.splits;
+    const std::uint32_t qb = p.qblocks - 1 - blockIdx.x / p.heads / p.splits;
     const std::uint32_t t0 = qb * kTok;
     const std::uint32_t t_end = t0 + kTok < p.tq ? t0 + kTok : p.tq;
     const std::uint32_t past = p.kv_len - p.tq;
     const std::uint32_t last_key = past + t_end - 1;
     const std::uint32_t ntiles = last_key / kPfTile + 1;
+    // This split's tiles [tile_begin, tile_end). The split holding the tile of
+    // the first row's position runs to the last tile and later splits are
+    // empty, so every split a workgroup runs starts at a key all its rows see
+    // (each row then sets its reference point on the first half-tile).
+    const std::uint32_t first_row_tile = (past + t0) / kPfTile;
+    std::uint32_t tile_begin = split * p.split_tiles;
+    std::uint32_t tile_end = tile_begin + p.split_tiles;
+    if (tile_end > first_row_tile) tile_end = ntiles;
+    if (tile_begin > first_row_tile) tile_begin = tile_end;
     const std::uint32_t npages = ((ntiles * kPfTile - 1) >> p.bs_shift) + 1;
     const std::uint32_t tile_pages_shift = kPfTileShift - p.bs_shift;
     // The page list holds a window of kWin pages (whole tiles) at a time: page
@@ -200,7 +218,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
         }
     };
-    stage(0);
+    stage((tile_begin & ~win_mask) << tile_pages_shift);
 
     Vec qb_op[kPfNt][kSteps];
     std::uint32_t row_token[kPfNt];
@@ -403,9 +421,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             lds_barrier();
         }
     };
-    issue(0, std::integral_constant<int, 0>{});
-    for (std::uint32_t tile = 0; tile < ntiles; tile += 2) {
-        if (tile + 1 < ntiles) {
+    if (tile_begin < tile_end) issue(tile_begin, std::integral_constant<int, 0>{});  // uniform
+    for (std::uint32_t tile = tile_begin; tile < tile_end; tile += 2) {
+        if (tile + 1 < tile_end) {
             restage(tile + 1);
             issue(tile + 1, std::integral_constant<int, 1>{});
             wait_vm<2 * kDma>();
@@ -418,8 +436,8 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         compute_tile(tile, ktile0, vtile0);
         wait_lgkm0();
         lds_barrier();
-        if (tile + 1 >= ntiles) break;
-        if (tile + 2 < ntiles) {
+        if (tile + 1 >= tile_end) break;
+        if (tile + 2 < tile_end) {
             restage(tile + 2);
             issue(tile + 2, std::integral_constant<int, 0>{});
             wait_vm<2 * kDma>();
@@ -442,14 +460,59 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         const int g = b % kG;
         const std::uint32_t token = row_token[n];
         if (token < t_end) {
-            float* dst =
-                p.output + (static_cast<std::uint64_t>(token) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
+            const std::uint64_t row = static_cast<std::uint64_t>(token) * p.query_heads + kvh * p.q_group + p.q_first + g;
+            // One store path for both cases (two would hold the accumulators
+            // twice): normalised rows of the output, or unnormalised partials.
+            const bool whole = p.splits == 1;
+            const std::uint64_t prow = static_cast<std::uint64_t>(split) * p.tq * p.query_heads + row;
+            float* dst = whole ? p.output + row * kD : p.part_o + prow * kD;
+            const float sc = whole ? inv : 1.0f;
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
                 *reinterpret_cast<float4*>(dst + 16 * dt + 4 * quad) =
-                    make_float4(acc[dt][n][0] * inv, acc[dt][n][1] * inv, acc[dt][n][2] * inv, acc[dt][n][3] * inv);
+                    make_float4(acc[dt][n][0] * sc, acc[dt][n][1] * sc, acc[dt][n][2] * sc, acc[dt][n][3] * sc);
             }
+            // An empty split leaves l = 0; the combine skips it.
+            if (!whole && quad == 0) *reinterpret_cast<float2*>(p.part_ml + 2 * prow) = make_float2(-nref[n], l);
         }
+    }
+}
+
+// Merges the key splits of every (token, query head) row: weights
+// exp2(ref_s - max ref) over the splits that saw a key, O = sum w_s O_s /
+// sum w_s l_s. One wavefront per row, lane d4 holding dims 4*d4 .. +4.
+template <int kD>
+__global__ __launch_bounds__(256) void paged_prefill_combine_kernel(const float* __restrict__ part_o,
+                                                                    const float* __restrict__ part_ml,
+                                                                    float* __restrict__ output, std::uint64_t rows,
+                                                                    std::uint32_t splits) {
+    const std::uint64_t row = static_cast<std::uint64_t>(blockIdx.x) * 4 + threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    if (row >= rows) return;
+    float m = -INFINITY;
+    for (std::uint32_t sp = 0; sp < splits; ++sp) {
+        const float2 ml = *reinterpret_cast<const float2*>(part_ml + 2 * (sp * rows + row));
+        if (ml.y > 0.0f) m = fmaxf(m, ml.x);
+    }
+    constexpr int kLanes = kD / 4;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float l = 0.0f;
+    for (std::uint32_t sp = 0; sp < splits; ++sp) {
+        const float2 ml = *reinterpret_cast<const float2*>(part_ml + 2 * (sp * rows + row));
+        if (!(ml.y > 0.0f)) continue;  // uniform: no key of this split is visible to the row
+        const float w = __builtin_amdgcn_exp2f(ml.x - m);
+        l += w * ml.y;
+        if (lane < kLanes) {
+            const float4 x = *reinterpret_cast<const float4*>(part_o + (sp * rows + row) * kD + 4 * lane);
+            o.x += w * x.x;
+            o.y += w * x.y;
+            o.z += w * x.z;
+            o.w += w * x.w;
+        }
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    if (lane < kLanes) {
+        *reinterpret_cast<float4*>(output + row * kD + 4 * lane) = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
     }
 }
 
@@ -458,7 +521,8 @@ int launch_prefill_pass(const PrefillParams& p, hipStream_t s) {
     PrefillParams q = p;
     constexpr unsigned kTok = 16 * (kPfWaves * pf_blocks_per_wave<kD>() / kG);
     q.qblocks = (p.tq + kTok - 1) / kTok;
-    hipLaunchKernelGGL((paged_prefill_kernel<E, kD, kG>), dim3(q.qblocks * p.heads), dim3(kPfThreads), 0, s, q);
+    hipLaunchKernelGGL((paged_prefill_kernel<E, kD, kG>), dim3(q.qblocks * p.heads * p.splits), dim3(kPfThreads), 0,
+                       s, q);
     return launch_status("paged_prefill_kernel");
 }
 
@@ -502,6 +566,12 @@ int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_
         }
         if (st != KVFLUX_OK) return st;
     }
+    if (p.splits > 1) {
+        const std::uint64_t rows = static_cast<std::uint64_t>(p.tq) * p.query_heads;
+        hipLaunchKernelGGL(paged_prefill_combine_kernel<kD>, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
+                           s, p.part_o, p.part_ml, p.output, rows, p.splits);
+        return launch_status("paged_prefill_combine_kernel");
+    }
     return KVFLUX_OK;
 }
 
@@ -514,16 +584,45 @@ int launch_prefill_head_size(const PrefillParams& p, std::uint64_t head_size, st
     }
 }
 
+struct PrefillPlan {
+    std::uint32_t splits;       // key splits per (query block, kv head)
+    std::uint32_t split_tiles;  // 64-key tiles per split
+    std::uint64_t workspace;    // bytes of partials (0 when splits == 1)
+};
+
+// Key splits for a call whose launches hold fewer workgroups than about two
+// per CU (short query blocks against a long prefix, as in chunked prefill):
+// enough splits for ~512 workgroups, each of at least 4 tiles (256 keys), at
+// most 32. Partials: [splits][tq][query_heads] rows of D floats, then the
+// same rows of {reference point, weight sum}.
+inline PrefillPlan prefill_plan(std::uint64_t head_size, std::uint64_t group, std::uint64_t num_kv_heads,
+                                std::uint64_t kv_len, std::uint64_t query_tokens, std::uint64_t query_heads) {
+    const std::uint64_t blocks = head_size == 256 ? kPfWaves : 2 * kPfWaves;
+    const std::uint64_t sub = prefill_sub_group(static_cast<std::uint32_t>(group), static_cast<std::uint32_t>(blocks));
+    const std::uint64_t tok = 16 * (blocks / sub);
+    const std::uint64_t wgs = (query_tokens + tok - 1) / tok * num_kv_heads;
+    const std::uint64_t tiles = (kv_len + kPfTile - 1) / kPfTile;
+    std::uint64_t splits = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;
+    if (splits > 32) splits = 32;
+    if (splits > tiles / 4) splits = tiles / 4;
+    if (splits < 1) splits = 1;
+    const std::uint64_t split_tiles = (tiles + splits - 1) / splits;
+    splits = (tiles + split_tiles - 1) / split_tiles;
+    const std::uint64_t ws = splits > 1 ? splits * query_tokens * query_heads * (head_size + 2) * sizeof(float) : 0;
+    return {static_cast<std::uint32_t>(splits), static_cast<std::uint32_t>(split_tiles), ws};
+}
+
 } // namespace
 } // namespace kvflux_hip
 
 using namespace kvflux_hip;
 
-extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_blocks,
-                                    uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size, int dtype,
-                                    const uint64_t* block_table, uint64_t num_table_blocks, uint64_t kv_len,
-                                    uint64_t query_tokens, uint64_t query_heads, const float* query,
-                                    float* output, void* stream) {
+namespace {
+
+int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_blocks, uint64_t num_kv_heads,
+                  uint64_t block_size, uint64_t head_size, int dtype, const uint64_t* block_table,
+                  uint64_t num_table_blocks, uint64_t kv_len, uint64_t query_tokens, uint64_t query_heads,
+                  const float* query, float* output, void* workspace, uint64_t workspace_bytes, void* stream) {
     if (query_tokens == 0) return KVFLUX_OK;
     if (dtype_bytes(dtype) == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
     if (!key_cache || !value_cache || !block_table || !query || !output) {
@@ -560,8 +659,59 @@ extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cac
     p.query = query;
     p.output = output;
     p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_size)));
+    p.splits = 1;
+    p.split_tiles = static_cast<std::uint32_t>((kv_len + kPfTile - 1) / kPfTile);
+    if (workspace) {
+        const PrefillPlan plan = prefill_plan(head_size, group, num_kv_heads, kv_len, query_tokens, query_heads);
+        if (plan.splits > 1) {
+            if (workspace_bytes < plan.workspace) {
+                return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill: workspace of %llu bytes, %llu needed",
+                            static_cast<unsigned long long>(workspace_bytes),
+                            static_cast<unsigned long long>(plan.workspace));
+            }
+            p.splits = plan.splits;
+            p.split_tiles = plan.split_tiles;
+            p.part_o = static_cast<float*>(workspace);
+            p.part_ml = p.part_o + static_cast<std::uint64_t>(plan.splits) * query_tokens * query_heads * head_size;
+        }
+    }
     const hipStream_t s = as_stream(stream);
     const std::uint32_t g = static_cast<std::uint32_t>(group);
     if (dtype == KVFLUX_DTYPE_BF16) return launch_prefill_head_size<PfBf16>(p, head_size, g, s);
     return launch_prefill_head_size<PfF16>(p, head_size, g, s);
+}
+
+} // namespace
+
+extern "C" int kvflux_paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_blocks,
+                                    uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size, int dtype,
+                                    const uint64_t* block_table, uint64_t num_table_blocks, uint64_t kv_len,
+                                    uint64_t query_tokens, uint64_t query_heads, const float* query,
+                                    float* output, void* stream) {
+    return paged_prefill(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype, block_table,
+                         num_table_blocks, kv_len, query_tokens, query_heads, query, output, nullptr, 0, stream);
+}
+
+extern "C" int kvflux_paged_prefill_workspace_size(uint64_t num_kv_heads, uint64_t head_size, uint64_t kv_len,
+                                                   uint64_t query_tokens, uint64_t query_heads, size_t* bytes) {
+    if (!bytes) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill workspace: null pointer");
+    *bytes = 0;
+    if (query_tokens == 0 || num_kv_heads == 0 || query_heads == 0 || query_heads % num_kv_heads != 0 ||
+        (head_size != 64 && head_size != 128 && head_size != 256) || kv_len == 0 || kv_len > 0x7fffffffULL ||
+        query_tokens > kv_len || query_heads > 0xffffffffULL) {
+        return KVFLUX_OK;  // no split launch for such a call
+    }
+    *bytes = static_cast<size_t>(
+        prefill_plan(head_size, query_heads / num_kv_heads, num_kv_heads, kv_len, query_tokens, query_heads).workspace);
+    return KVFLUX_OK;
+}
+
+extern "C" int kvflux_paged_prefill_split(const void* key_cache, const void* value_cache, uint64_t num_blocks,
+                                          uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size, int dtype,
+                                          const uint64_t* block_table, uint64_t num_table_blocks, uint64_t kv_len,
+                                          uint64_t query_tokens, uint64_t query_heads, const float* query,
+                                          float* output, void* workspace, uint64_t workspace_bytes, void* stream) {
+    return paged_prefill(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype, block_table,
+                         num_table_blocks, kv_len, query_tokens, query_heads, query, output, workspace,
+                         workspace_bytes, stream);
 }

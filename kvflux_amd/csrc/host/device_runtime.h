@@ -188,4 +188,14 @@ inline void* attention_workspace(const PagedKVStorage& storage, std::size_t rows
     return *bytes ? storage.scratch().workspace.reserve(*bytes) : nullptr;
 }
 
+// Workspace of the split-key MFMA prefill (nullptr when the call does not split).
+inline void* prefill_workspace(const PagedKVStorage& storage, std::size_t query_tokens, std::size_t kv_len,
+                               std::size_t query_heads, std::size_t* bytes) {
+    const auto& layout = storage.layout();
+    check(kvflux_paged_prefill_workspace_size(layout.num_kv_heads(), layout.head_size(), kv_len, query_tokens,
+                                              query_heads, bytes),
+          "prefill workspace size");
+    return *bytes ? storage.scratch().workspace.reserve(*bytes) : nullptr;
+}
+
 } // namespace kvflux::v2::detail

@@ -20,6 +20,7 @@ namespace {
 
 using detail::abi_dtype;
 using detail::attention_workspace;
+using detail::prefill_workspace;
 using detail::check;
 using detail::mul_checked;
 using detail::validate_q_o;
@@ -225,11 +226,13 @@ void paged_attention(const PagedKVStorage& storage, const SequenceState& sequenc
     const auto dev = storage.scratch().upload({{table.data(), table_bytes}});
     bool launched = false;
     if (prefill_eligible(layout, query_tokens, precision)) {
-        const int status = kvflux_paged_prefill(
+        std::size_t ws_bytes = 0;
+        void* ws = prefill_workspace(storage, query_tokens, sequence.num_tokens(), query_heads, &ws_bytes);
+        const int status = kvflux_paged_prefill_split(
             storage.key_base(), storage.value_base(), layout.num_blocks(), layout.num_kv_heads(),
             layout.block_size(), layout.head_size(), abi_dtype(layout.dtype()), dev[0],
             table.size(), sequence.num_tokens(), query_tokens, query_heads, query_device,
-            output_device, nullptr);
+            output_device, ws, ws_bytes, nullptr);
         // A shape the MFMA kernel declines runs on the FP32 kernel instead.
         if (status != KVFLUX_ERR_UNSUPPORTED) check(status, "paged prefill kernel launch");
         launched = status == KVFLUX_OK;

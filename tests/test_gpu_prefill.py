@@ -183,11 +183,15 @@ def test_prefill_through_cpp_layer(gpu, v2, kv_heads, q_heads):
     exp = oracle.paged_attention_causal(kh, vh, kv_heads, 16, 128, oracle.BF16, table, 500, q, 500, q_heads,
                                         threads=8)
     assert np.abs(got - exp).max() < 2e-2
-    # the same bits as the MFMA kernel called through the C ABI
+    # the same bits as the MFMA kernel called through the C ABI (with the
+    # workspace that lets it split the keys, as the C++ layer does)
     td, od2 = buffer_like(table), buffer_like(np.zeros(q.size, np.float32))
-    assert capi.lib().kvflux_paged_prefill(storage.key_base(), storage.value_base(), 64, kv_heads, 16, 128,
-                                           capi.DTYPE_BF16, td.ptr, len(table), 500, 500, q_heads, qd.ptr,
-                                           od2.ptr, None) == 0
+    ws = C.c_size_t(0)
+    capi.check(capi.lib().kvflux_paged_prefill_workspace_size(kv_heads, 128, 500, 500, q_heads, C.byref(ws)))
+    wd = device.DeviceBuffer(max(ws.value, 16))
+    assert capi.lib().kvflux_paged_prefill_split(storage.key_base(), storage.value_base(), 64, kv_heads, 16, 128,
+                                                 capi.DTYPE_BF16, td.ptr, len(table), 500, 500, q_heads, qd.ptr,
+                                                 od2.ptr, wd.ptr, ws.value, None) == 0
     device.synchronize()
     assert np.array_equal(od2.download(np.float32).view(np.uint32), got.view(np.uint32))
 
@@ -221,6 +225,55 @@ def test_precision_routing(gpu, v2):
         assert np.abs(out[P.Exact].view(np.float32) - exp).max() < 1e-5
         assert np.abs(out[P.Fast].view(np.float32) - exp).max() < 2e-2
     assert not np.array_equal(out[P.Fast], out[P.Exact])  # two different kernels
+
+
+SPLIT_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
+    ("BFloat16", 8, 32, 128, 16, 8192, 64),    # chunked prefill against a long prefix
+    ("BFloat16", 2, 8, 128, 16, 5126, 100),    # split 16 starts at key 5120, inside the last
+                                               # block's diagonal (rows 5090..5119 see none of it)
+    ("Float16", 1, 16, 128, 16, 3000, 40),     # group 16, one token block per workgroup
+    ("BFloat16", 2, 20, 64, 32, 4000, 77),     # group 10 as 2 x 5 passes, then one combine
+    ("BFloat16", 1, 2, 256, 16, 6000, 48),
+    ("BFloat16", 1, 4, 128, 1, 20000, 16),     # page-list windows inside splits
+]
+
+
+@pytest.mark.parametrize("name,kv_heads,q_heads,head_size,bs,kv_len,q_tokens", SPLIT_CASES)
+def test_prefill_split_keys(gpu, name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens):
+    """kvflux_paged_prefill_split: the keys of each (query block, kv head)
+    spread over several workgroups and merged by the combine kernel. Matches
+    the oracle (2e-2), the float64 emulation (4e-3) and the unsplit kernel."""
+    blocks = (kv_len + bs - 1) // bs + 17
+    seed = kv_len + 3 * q_tokens
+    kc, vc, table = setup_case(name, blocks, kv_heads, bs, head_size, kv_len, seed)
+    q = oracle.random_elements(0, q_tokens * q_heads * head_size, oracle.F32, 1, seed)
+    lib = capi.lib()
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_prefill_workspace_size(kv_heads, head_size, kv_len, q_tokens, q_heads, C.byref(ws)))
+    assert ws.value > 0  # the call splits
+    td, qd = buffer_like(table), buffer_like(q)
+    wd = device.DeviceBuffer(ws.value)
+    od = buffer_like(np.full(q.size + 4, 777.0, np.float32))
+    assert lib.kvflux_paged_prefill_split(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, CODES[name], td.ptr,
+                                          len(table), kv_len, q_tokens, q_heads, qd.ptr, od.ptr, wd.ptr, ws.value,
+                                          None) == 0, capi.last_error()
+    assert lib.kvflux_paged_prefill_split(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, CODES[name], td.ptr,
+                                          len(table), kv_len, q_tokens, q_heads, qd.ptr, od.ptr, wd.ptr,
+                                          ws.value - 1, None) == capi.ERR_INVALID
+    device.synchronize()
+    out = od.download(np.float32)
+    assert np.all(out[q.size:] == 777.0)
+    got = out[:q.size]
+    assert np.all(np.isfinite(got))
+    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    exp = oracle.paged_attention_causal(kh, vh, kv_heads, bs, head_size, CODES[name], table, kv_len, q, q_tokens,
+                                        q_heads, threads=8)
+    assert np.abs(got - exp).max() < 2e-2
+    rows = sorted({0, 1, q_tokens // 2, q_tokens - 2, q_tokens - 1} & set(range(q_tokens)))
+    emu = emulate(kh, vh, name, kv_heads, bs, head_size, table, kv_len, q, q_tokens, q_heads, rows)
+    assert np.abs(got.reshape(q_tokens, q_heads, head_size)[rows] - emu).max() < 4e-3
+    whole = run_prefill(name, kc, vc, blocks, kv_heads, bs, head_size, table, kv_len, q, q_tokens, q_heads)
+    assert np.abs(got - whole).max() < 4e-3
 
 
 GAP_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens, missing table entries
