@@ -235,6 +235,8 @@ SPLIT_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("BFloat16", 2, 20, 64, 32, 4000, 77),     # group 10 as 2 x 5 passes, then one combine
     ("BFloat16", 1, 2, 256, 16, 6000, 48),
     ("BFloat16", 1, 4, 128, 1, 20000, 16),     # page-list windows inside splits
+    ("BFloat16", 2, 8, 128, 16, 3000, 1),      # one query token (Fast precision sends it here)
+    ("Float16", 1, 6, 64, 64, 2500, 2),        # group 6 with two tokens
 ]
 
 
