@@ -6,7 +6,9 @@
 // heads (G <= 8, or 16 when R = 16; the row blocks past R / G * G idle when G
 // does not divide R; other GQA groups run as passes over sub-groups of G
 // heads). Wavefront w owns row blocks R/8 * w .. (row block b = head b % G,
-// tokens 16 * (b / G) ..). Keys stream through
+// tokens 16 * (b / G) ..). A call that would not fill the GPU (short query
+// blocks against a long prefix) may spread each workgroup's keys over several
+// workgroups, merged by paged_prefill_combine_kernel. Keys stream through
 // LDS in tiles of 64, double-buffered: K and V go from global memory straight
 // into LDS (global_load_lds_dwordx4, no staging registers and no LDS write
 // instructions), the next tile's loads in flight while this tile is computed
