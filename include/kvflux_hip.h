@@ -165,7 +165,7 @@ int kvflux_paged_attention(const void* key_cache, const void* value_cache,
  * Q is rounded to the cache dtype and the softmax weights to the cache dtype
  * before the MFMA products; accumulation and softmax are FP32.
  * KVFLUX_ERR_UNSUPPORTED unless dtype is F16/BF16, head_size is 64, 128 or
- * 256, block_size divides 64 and kv_len is below 2^31. Any GQA group query_heads / num_kv_heads:
+ * 256, block_size is a power of two up to 256 and kv_len is below 2^31. Any GQA group query_heads / num_kv_heads:
  * groups 1..8 (and 16 at head_size 64/128) in one launch, others as one
  * launch per sub-group of heads (the largest divisor of the group among
  * 16, 8, 7, ..., 1 that one launch takes).

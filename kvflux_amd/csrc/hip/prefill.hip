@@ -88,14 +88,13 @@ constexpr int pf_blocks_per_wave() { return kD == 256 ? 1 : 2; }
 constexpr int kPfTileShift = 6;
 constexpr int kPfTile = 1 << kPfTileShift;  // keys per LDS tile
 // Page ids held in LDS per workgroup, one window of the sequence at a time:
-// 8192 (32 KiB) beside the 64 KiB of tiles at head_size <= 128, 4096 beside
-// the 128 KiB at 256.
+// 2048 (8 KiB, 32K tokens at block_size 16) beside the tiles.
 template <int kD>
-constexpr int pf_table_max() { return kD == 256 ? 4096 : 8192; }
+constexpr int pf_table_max() { return 2048; }
 // Flag bit of a missing page in the LDS page list (ids are below 2^31): its
 // K and V rows are loaded from pf_zero_rows instead.
 constexpr std::uint32_t kPfMissing = 0x80000000u;
-// One head's rows of one page at block_size <= 64 and head_size <= 256
+// The rows of one 64-key tile at head_size <= 256
 // (16-bit elements): the source of missing pages, all zeros.
 constexpr int kPfZeroBytes = 64 * 512;
 __device__ __attribute__((aligned(16))) unsigned char pf_zero_rows[kPfZeroBytes];
@@ -206,12 +205,14 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     if (tile_end > first_row_tile) tile_end = ntiles;
     if (tile_begin > first_row_tile) tile_begin = tile_end;
     const std::uint32_t npages = ((ntiles * kPfTile - 1) >> p.bs_shift) + 1;
-    const std::uint32_t tile_pages_shift = kPfTileShift - p.bs_shift;
+    // Key k of the sequence lies in page k >> bs_shift, row k & (bs - 1).
     // The page list holds a window of kWin pages (whole tiles) at a time: page
     // `first` + i at pages[i]. A prompt longer than one window is restaged at
     // each window boundary of the tile loop.
     constexpr std::uint32_t kWin = pf_table_max<kD>();
-    const std::uint32_t win_mask = (kWin >> tile_pages_shift) - 1;  // tiles per window - 1
+    // Tiles per window - 1 (windows start at multiples of kWin pages).
+    const std::uint32_t win_mask = static_cast<std::uint32_t>((static_cast<std::uint64_t>(kWin) << p.bs_shift) >> kPfTileShift) - 1;
+    auto first_page = [&](std::uint32_t tile) { return (tile << kPfTileShift) >> p.bs_shift; };
     auto stage = [&](std::uint32_t first) {
         for (std::uint32_t i = tid; i < kWin && first + i < npages; i += kPfThreads) {
             const std::uint32_t pg = first + i;
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
         }
     };
-    stage((tile_begin & ~win_mask) << tile_pages_shift);
+    stage(first_page(tile_begin & ~win_mask));
 
     Vec qb_op[kPfNt][kSteps];
     std::uint32_t row_token[kPfNt];
@@ -253,27 +254,32 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     // slot ^ vswz(row), so reads below see the swizzled layout.
     const char* kc = static_cast<const char*>(p.key_cache);
     const char* vc = static_cast<const char*>(p.value_cache);
+    // Below 2^32 (the host declines larger pages).
     const std::uint32_t page_bytes = (static_cast<std::uint32_t>(kRowBytes) << p.bs_shift) * p.heads;
     const std::uint32_t head_bytes = (kvh << p.bs_shift) * kRowBytes;
     const std::uint32_t in_page_mask = (1u << p.bs_shift) - 1;
     auto kswz = [](int row) { return kCpr == 16 ? (row & 15) : ((row >> 1) & 7); };
     auto vswz = [](int row) { return kVSwz * (row & 7); };
     auto issue = [&](std::uint32_t tile, auto buf) {
+        // Key tile * 64 + row: page (tile * 64 >> bs_shift) + (row >> bs_shift)
+        // and row (tile * 64 & (bs - 1)) + (row & (bs - 1)) of it, the tile's
+        // terms wave-uniform (tile * 64 is a multiple of bs, or bs of 64).
+        const std::uint32_t tile_page = ((tile & win_mask) << kPfTileShift) >> p.bs_shift;  // within the window
+        const std::uint32_t tile_bytes = head_bytes + ((tile << kPfTileShift) & in_page_mask) * kRowBytes;
 #pragma unroll
         for (int i = 0; i < kDma; ++i) {
             const int e = (i * kPfWaves + wave) * 64 + lane;
             const int row = e / kCpr, slot = e % kCpr;
             const std::uint32_t r = static_cast<std::uint32_t>(row) & in_page_mask;
-            const std::uint32_t entry =
-                pages[((tile & win_mask) << tile_pages_shift) + (static_cast<std::uint32_t>(row) >> p.bs_shift)];
+            const std::uint32_t entry = pages[tile_page + (static_cast<std::uint32_t>(row) >> p.bs_shift)];
             const std::uint32_t kchunk = (slot ^ kswz(row)) * 16, vchunk = (slot ^ vswz(row)) * 16;
             const char* ks;
             const char* vs;
             if (entry & kPfMissing) {
-                ks = reinterpret_cast<const char*>(pf_zero_rows) + r * kRowBytes + kchunk;
-                vs = reinterpret_cast<const char*>(pf_zero_rows) + r * kRowBytes + vchunk;
+                ks = reinterpret_cast<const char*>(pf_zero_rows) + row * kRowBytes + kchunk;
+                vs = reinterpret_cast<const char*>(pf_zero_rows) + row * kRowBytes + vchunk;
             } else {
-                const std::uint64_t base = static_cast<std::uint64_t>(entry) * page_bytes + head_bytes + r * kRowBytes;
+                const std::uint64_t base = static_cast<std::uint64_t>(entry) * page_bytes + tile_bytes + r * kRowBytes;
                 ks = kc + base + kchunk;
                 vs = vc + base + vchunk;
             }
@@ -418,7 +424,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     // barrier that ended the previous step.
     auto restage = [&](std::uint32_t next) {
         if ((next & win_mask) == 0) {  // uniform
-            stage(next << tile_pages_shift);
+            stage(first_page(next));
             wait_lgkm0();
             lds_barrier();
         }
@@ -640,8 +646,8 @@ int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_b
     }
     const std::uint64_t group = query_heads / num_kv_heads;
     if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128 && head_size != 256) || !is_pow2(block_size) ||
-        block_size > 64 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0x7fffffffULL ||
-        query_heads > 0xffffffffULL) {
+        block_size > 256 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0x7fffffffULL ||
+        query_heads > 0xffffffffULL || num_kv_heads * block_size * head_size * 2 > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
     }
 

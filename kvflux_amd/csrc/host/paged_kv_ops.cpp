@@ -181,7 +181,8 @@ bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens,
     if (precision == AttentionPrecision::Exact) return false;
     if (layout.dtype() == DType::Float32) return false;
     if (layout.head_size() != 64 && layout.head_size() != 128 && layout.head_size() != 256) return false;
-    if (64 % layout.block_size() != 0) return false;
+    const std::size_t bs = layout.block_size();
+    if (bs > 256 || (bs & (bs - 1)) != 0) return false;  // a power of two up to 256
     if (precision == AttentionPrecision::Auto && query_tokens < 16) return false;
     return query_tokens >= 1;
 }

@@ -111,6 +111,10 @@ CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("BFloat16", 1, 4, 64, 1, 20000, 300),
     ("Float16", 1, 2, 256, 4, 40000, 40),
     ("BFloat16", 2, 8, 128, 16, 140000, 16),
+    # pages longer than a 64-key tile (a tile is part of one page)
+    ("BFloat16", 2, 8, 128, 128, 1000, 1000),
+    ("Float16", 1, 4, 64, 256, 700, 300),
+    ("BFloat16", 1, 2, 256, 128, 9000, 40),
 ]
 
 
@@ -237,6 +241,7 @@ SPLIT_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("BFloat16", 1, 4, 128, 1, 20000, 16),     # page-list windows inside splits
     ("BFloat16", 2, 8, 128, 16, 3000, 1),      # one query token (Fast precision sends it here)
     ("Float16", 1, 6, 64, 64, 2500, 2),        # group 6 with two tokens
+    ("BFloat16", 2, 8, 128, 128, 6000, 64),    # 128-token pages
 ]
 
 
@@ -282,6 +287,7 @@ GAP_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens, missi
     ("BFloat16", 2, 8, 128, 4, 500, 500, [3, 40, 124]),
     ("Float16", 1, 8, 64, 8, 333, 120, [0, 20, 41]),
     ("BFloat16", 2, 4, 128, 1, 130, 130, [7, 129]),
+    ("BFloat16", 2, 8, 128, 128, 700, 700, [1, 5]),
 ]
 
 
