@@ -444,10 +444,72 @@ def bench_write(v2, args, stream):
         gv = device.memcpy_d2h(vb + pg * page_elems * 2, page_elems * 2, np.uint16)
         mism += int((gk != host_k[j * page_elems:(j + 1) * page_elems]).sum())
         mism += int((gv != host_v[j * page_elems:(j + 1) * page_elems]).sum())
-    del seqs
     bytes_step = 2 * 2 * N * H * D * 2 + N * 8
+    cold = bench_write_cold(v2, args, stream, pool, storage, rng)
+    del seqs
     return {"kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9, "bytes": bytes_step,
-            "api_us": api_us, "tokens": N, "pages_checked": int(pages.size), "mismatched_elements": mism}
+            "api_us": api_us, "tokens": N, "pages_checked": int(pages.size), "mismatched_elements": mism,
+            "cold": cold}
+
+
+def bench_write_cold(v2, args, stream, pool, storage, rng, sets: int = 16):
+    """The same write with its working set rotated through `sets` distinct
+    (K_new, V_new, slots) triples, 16 x 33.6 MB = 537 MB in all: more than
+    the 256 MB Infinity Cache, so every launch reads inputs and writes pages
+    that no earlier launch of the cycle touched. Each set is 256 sequences of
+    16 new tokens at a prefix length ~ U[0, 64) (uniform in-page offsets,
+    pages from the same seeded permutation), on pages no other set uses."""
+    from kvflux_amd import capi, device
+    from oracle import oracle
+
+    N_SEQ, NEW, H, D, bs = 256, 16, 8, 128, 16
+    n = N_SEQ * NEW * H * D
+    lib = capi.lib()
+    kb, vb = storage.key_base(), storage.value_base()
+    bufs, seqs = [], []
+    for j in range(sets):
+        writes = []
+        for i, L0 in enumerate(rng.integers(0, 64, N_SEQ).tolist()):
+            s = v2.SequenceState(10**6 + j * N_SEQ + i, pool)
+            s.append_tokens(L0 + NEW)
+            seqs.append(s)
+            writes += [(s, L0 + t) for t in range(NEW)]
+        slots = np.array(v2.build_slot_mapping(writes), np.uint64)
+        kn, vn = device.DeviceBuffer(n * 2), device.DeviceBuffer(n * 2)
+        device.fill_random(kn.ptr, n, capi.DTYPE_BF16, 1, args.seed + 100 + 2 * j)
+        device.fill_random(vn.ptr, n, capi.DTYPE_BF16, 1, args.seed + 101 + 2 * j)
+        bufs.append((kn, vn, device.to_device(slots), slots))
+    device.synchronize()
+    cycle = [0]
+
+    def launch():
+        kn, vn, sd, _ = bufs[cycle[0] % sets]
+        cycle[0] += 1
+        capi.check(lib.kvflux_write_paged_kv(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16,
+                                             kn.ptr, vn.ptr, sd.ptr, N_SEQ * NEW, stream))
+
+    ms = time_launches(launch, stream, sets, sets * max(4, args.steps // 4))
+    # Every set's pages hold that set's rows: check two sets bit-exactly.
+    page_elems = H * bs * D
+    mism = 0
+    for j in (0, sets - 1):
+        kn, vn, _, slots = bufs[j]
+        pages = np.unique(slots // bs)
+        remap = {int(p): i for i, p in enumerate(pages.tolist())}
+        local = np.array([remap[int(s // bs)] * bs + int(s % bs) for s in slots], np.uint64)
+        host_k = np.concatenate([device.memcpy_d2h(kb + int(p) * page_elems * 2, page_elems * 2, np.uint16)
+                                 for p in pages])
+        host_v = np.concatenate([device.memcpy_d2h(vb + int(p) * page_elems * 2, page_elems * 2, np.uint16)
+                                 for p in pages])
+        exp_k, exp_v = host_k.copy(), host_v.copy()
+        oracle.write_paged_kv(exp_k, exp_v, H, bs, D, oracle.BF16, kn.download(np.uint16), vn.download(np.uint16),
+                              local)
+        mism += int((exp_k != host_k).sum() + (exp_v != host_v).sum())
+    del seqs
+    bytes_step = 2 * 2 * N_SEQ * NEW * H * D * 2 + N_SEQ * NEW * 8
+    return {"kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9, "sets": sets,
+            "working_set_bytes": sets * bytes_step, "sets_checked": 2, "mismatched_elements": mism,
+            "pct_of_peak": round(100 * bytes_step / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2)}
 
 
 # --------------------------------------------------------------------- gather
@@ -624,6 +686,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-rows", type=int, default=24, help="decode rows timed on the CPU oracle")
     ap.add_argument("--skip-aux", action="store_true", help="decode only")
+    ap.add_argument("--only", choices=("write", "gather", "prefill", "cow"),
+                    help="run one auxiliary leg alone and print its JSON object (for profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true", help="1 GiB device copy for counter scaling")
     args = ap.parse_args()
     if args.calibrate_copy:
@@ -645,6 +709,15 @@ def main() -> int:
         return 1
     capi.call("kvflux_set_device", 0)
     stream = device.Stream()
+
+    if args.only:
+        legs = {"write": lambda: bench_write(v2, args, stream.handle),
+                "gather": lambda: bench_gather(v2, args, stream.handle, "BFloat16"),
+                "prefill": lambda: bench_prefill(v2, args, stream.handle),
+                "cow": lambda: bench_cow(v2, args, stream.handle)}
+        log(f"{args.only} ...")
+        print(json.dumps({args.only: legs[args.only]()}))
+        return 0
 
     log("decode ...")
     dec = bench_decode(v2, args, stream.handle)
