@@ -26,6 +26,7 @@
 //    combines in chunk order, so results are bit-reproducible.
 #include "common.h"
 
+#include <atomic>
 #include <cmath>
 #include <type_traits>
 
@@ -1150,21 +1151,165 @@ __global__ __launch_bounds__(64) void paged_attention_generic_kernel(Params p, s
 }
 
 // ---------------------------------------------------------------- dispatch
+//
+// A call is planned first and launched second. The plan fixes the kernel
+// family, the GQA sub-group of the block-size-16 kernel, its work-item size
+// and so the number of chunk partials per (row, query head), which is the
+// stride of the partial arrays. Both entry points (caller workspace, static
+// scratch) launch the same plan.
+
+// Resident workgroups of one kernel on one device (CUs x occupancy), queried
+// once per (kernel, device). Devices past kMaxDevices are queried per call.
+constexpr int kMaxDevices = 64;
+
 template <typename E, int kD, int kG>
-int launch_split(Params p, std::uint64_t rows, std::uint64_t max_chunks, hipStream_t s) {
+int resident_slots(int* out) {
+    static std::atomic<int> cache[kMaxDevices];
+    int device = 0;
+    int status = hip_status(hipGetDevice(&device), "hipGetDevice");
+    if (status != KVFLUX_OK) return status;
+    if (device >= 0 && device < kMaxDevices) {
+        const int known = cache[device].load(std::memory_order_relaxed);
+        if (known > 0) {
+            *out = known;
+            return KVFLUX_OK;
+        }
+    }
+    int cus = 0, per_cu = 0;
+    status = hip_status(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                        "hipDeviceGetAttribute");
+    if (status == KVFLUX_OK)
+        status = hip_status(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                &per_cu, paged_decode_bs16_kernel<E, kD, kG>, kThreads, 0),
+                            "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (status != KVFLUX_OK) return status;
+    const int slots = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+    if (device >= 0 && device < kMaxDevices) cache[device].store(slots, std::memory_order_relaxed);
+    *out = slots;
+    return KVFLUX_OK;
+}
+
+enum class Family { Bs16, Split, Generic };
+
+struct Plan {
+    Family family = Family::Generic;
+    std::uint32_t sub = 0;     // Bs16: query heads per launch (divides the group, <= 8)
+    std::uint32_t shift = 9;   // Bs16: log2(tokens per work item)
+    unsigned grid = 0;         // Bs16: persistent grid
+    std::uint64_t chunks = 0;  // partial slots per (row, query head); <= 1: no partials
+};
+
+template <typename E, int kD>
+int resident_slots_for(std::uint32_t sub, int* out) {
+    switch (sub) {
+    case 1: return resident_slots<E, kD, 1>(out);
+    case 2: return resident_slots<E, kD, 2>(out);
+    case 3: return resident_slots<E, kD, 3>(out);
+    case 4: return resident_slots<E, kD, 4>(out);
+    case 5: return resident_slots<E, kD, 5>(out);
+    case 6: return resident_slots<E, kD, 6>(out);
+    case 7: return resident_slots<E, kD, 7>(out);
+    default: return resident_slots<E, kD, 8>(out);
+    }
+}
+
+// max_chunks: ceil(kv_len / kChunk), the partial count at 512-token items.
+template <typename E, int kD>
+int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::uint64_t max_chunks,
+               Plan* plan) {
+    if constexpr (!std::is_same<E, F32>::value && (kD == 64 || kD == 128)) {
+        // The kernel counts work items in 32 bits (at most 512-token chunks);
+        // rows <= kPlanRows keeps the product below 2^51.
+        const std::uint32_t bs = p.block_size.divisor;
+        if ((bs == 16 || bs == 32 || bs == 64 || bs == 128) && rows <= kPlanRows && p.width > 0 &&
+            rows * max_chunks * p.heads <= 0xffffffffULL) {
+            // A group above 8 runs as launches of a sub-group: the largest
+            // divisor of the group up to 8, each launch serving its slice of
+            // the query heads (and reading K/V again); the chunk partials of
+            // all of them are combined once, after the last. Group 8 at
+            // kD = 128 takes 251 VGPRs (no spills, two workgroups per CU):
+            // 1.27 against 3.10 ms on the VALU split kernel for 128 rows of
+            // U[1024, 32768] tokens with 64 query / 8 kv heads.
+            const auto g = static_cast<std::uint32_t>(group);
+            std::uint32_t sub = g < 8 ? g : 8;
+            while (g % sub != 0) --sub;
+            int slots = 0;
+            const int status = resident_slots_for<E, kD>(sub, &slots);
+            if (status != KVFLUX_OK) return status;
+            // Work item size: the largest chunk (512, 1024, 2048 or 4096
+            // tokens) that still gives at least 8 items per resident
+            // workgroup when every row is kv_len long.
+            std::uint32_t shift = 9;
+            while (shift < 12) {
+                const std::uint64_t wider =
+                    ((p.kv_len + (std::uint64_t{2} << shift) - 1) >> (shift + 1)) * rows * p.heads;
+                if (wider < 8 * static_cast<std::uint64_t>(slots)) break;
+                ++shift;
+            }
+            const std::uint64_t chunks = (p.kv_len + (std::uint64_t{1} << shift) - 1) >> shift;
+            const std::uint64_t items = rows * chunks * p.heads;  // upper bound of the real count
+            plan->family = Family::Bs16;
+            plan->sub = sub;
+            plan->shift = shift;
+            plan->grid = static_cast<unsigned>(items == 0 ? 1 : items < static_cast<std::uint64_t>(slots) ? items : slots);
+            plan->chunks = chunks;
+            return KVFLUX_OK;
+        }
+    }
+    if (group == 1 || group == 2 || group == 4 || group == 8) {
+        plan->family = Family::Split;
+        plan->chunks = max_chunks;
+    } else {
+        plan->family = Family::Generic;
+        plan->chunks = 0;
+    }
+    return KVFLUX_OK;
+}
+
+template <typename E>
+int plan_call(const Params& p, std::uint64_t rows, std::uint64_t head_dim, std::uint64_t group,
+              std::uint64_t max_chunks, Plan* plan) {
+    switch (head_dim) {
+    case 64: return plan_group<E, 64>(p, rows, group, max_chunks, plan);
+    case 128: return plan_group<E, 128>(p, rows, group, max_chunks, plan);
+    case 256:
+        if (group <= 4) return plan_group<E, 256>(p, rows, group, max_chunks, plan);
+        break;
+    default: break;
+    }
+    plan->family = Family::Generic;
+    plan->chunks = 0;
+    return KVFLUX_OK;
+}
+
+int launch_combine(Params p, std::uint32_t head_dim, std::uint32_t chunk_tokens, hipStream_t s) {
+    const std::uint64_t per_launch = 0x7fffffffULL / p.query_heads;
+    for (std::uint64_t base = 0; base < p.num_rows; base += per_launch) {
+        const std::uint64_t n = p.num_rows - base < per_launch ? p.num_rows - base : per_launch;
+        p.row_base = static_cast<std::uint32_t>(base);
+        hipLaunchKernelGGL(paged_attention_combine_kernel, dim3(static_cast<unsigned>(n * p.query_heads)),
+                           dim3(kCombineThreads), 0, s, p, head_dim, chunk_tokens);
+        const int status = launch_status("paged_attention_combine_kernel");
+        if (status != KVFLUX_OK) return status;
+    }
+    return KVFLUX_OK;
+}
+
+template <typename E, int kD, int kG>
+int launch_split(Params p, std::uint64_t rows, hipStream_t s) {
     const std::uint64_t rows_per_launch = 65535 / p.heads;
     for (std::uint64_t base = 0; base < rows; base += rows_per_launch) {
         const std::uint64_t n = rows - base < rows_per_launch ? rows - base : rows_per_launch;
         p.row_base = static_cast<std::uint32_t>(base);
         hipLaunchKernelGGL((paged_attention_split_kernel<E, kD, kG>),
-                           dim3(static_cast<unsigned>(max_chunks), static_cast<unsigned>(n * p.heads)),
+                           dim3(p.max_chunks > 0 ? p.max_chunks : 1u, static_cast<unsigned>(n * p.heads)),
                            dim3(kThreads), 0, s, p);
         int status = launch_status("paged_attention_split_kernel");
         if (status != KVFLUX_OK) return status;
-        if (max_chunks > 1) {
+        if (p.max_chunks > 1) {
             hipLaunchKernelGGL(paged_attention_combine_kernel,
-                               dim3(static_cast<unsigned>(n * p.query_heads)), dim3(kCombineThreads), 0, s, p,
-                               static_cast<std::uint32_t>(kD), static_cast<std::uint32_t>(kChunk));
+                               dim3(static_cast<unsigned>(n * p.query_heads)), dim3(kCombineThreads), 0, s,
+                               p, static_cast<std::uint32_t>(kD), static_cast<std::uint32_t>(kChunk));
             status = launch_status("paged_attention_combine_kernel");
             if (status != KVFLUX_OK) return status;
         }
@@ -1187,116 +1332,65 @@ int launch_generic(Params p, std::uint64_t rows, std::uint64_t head_dim, hipStre
     return KVFLUX_OK;
 }
 
-// Persistent grid: every resident workgroup slot gets one workgroup.
 template <typename E, int kD, int kG>
-int launch_bs16(Params p, std::uint64_t max_chunks, hipStream_t s, bool combine) {
-    static int slots = 0;  // resident workgroups per device (queried once)
-    if (slots == 0) {
-        int device = 0, cus = 0, per_cu = 0;
-        int status = hip_status(hipGetDevice(&device), "hipGetDevice");
-        if (status == KVFLUX_OK)
-            status = hip_status(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
-                                "hipDeviceGetAttribute");
-        if (status == KVFLUX_OK)
-            status = hip_status(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                    &per_cu, paged_decode_bs16_kernel<E, kD, kG>, kThreads, 0),
-                                "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-        if (status != KVFLUX_OK) return status;
-        slots = cus * (per_cu > 0 ? per_cu : 1);
-    }
-    // Work item size: the largest chunk (512, 1024, 2048 or 4096 tokens)
-    // that still gives at least 8 items per resident workgroup when every
-    // row is kv_len long. Partial slots stay sized for 512-token chunks
-    // (max_chunks), an upper bound on the chunk count of any larger chunk.
-    std::uint32_t shift = 9;
-    while (shift < 12) {
-        const std::uint64_t wider = ((p.kv_len + (std::uint64_t{2} << shift) - 1) >> (shift + 1)) *
-                                    p.num_rows * p.heads;
-        if (wider < 8 * static_cast<std::uint64_t>(slots)) break;
-        ++shift;
-    }
-    p.chunk_shift = shift;
-    const std::uint64_t items = static_cast<std::uint64_t>(p.num_rows) * max_chunks * p.heads;
-    const unsigned grid = static_cast<unsigned>(items < static_cast<std::uint64_t>(slots) ? items : slots);
+int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
     p.row_base = 0;
-    hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG>), dim3(grid), dim3(kThreads), 0, s, p);
-    int status = launch_status("paged_decode_bs16_kernel");
-    if (status != KVFLUX_OK) return status;
-    if (combine && max_chunks > 1) {
-        for (std::uint64_t base = 0; base < p.num_rows; base += 0x7fffffffULL / p.query_heads) {
-            const std::uint64_t n = p.num_rows - base < 0x7fffffffULL / p.query_heads
-                                        ? p.num_rows - base : 0x7fffffffULL / p.query_heads;
-            p.row_base = static_cast<std::uint32_t>(base);
-            hipLaunchKernelGGL(paged_attention_combine_kernel, dim3(static_cast<unsigned>(n * p.query_heads)),
-                               dim3(kCombineThreads), 0, s, p, static_cast<std::uint32_t>(kD),
-                               static_cast<std::uint32_t>(1u << p.chunk_shift));
-            status = launch_status("paged_attention_combine_kernel");
-            if (status != KVFLUX_OK) return status;
+    hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG>), dim3(plan.grid), dim3(kThreads), 0, s, p);
+    return launch_status("paged_decode_bs16_kernel");
+}
+
+template <typename E, int kD>
+int run_bs16(Params p, const Plan& plan, hipStream_t s) {
+    const std::uint32_t bs = p.block_size.divisor;
+    p.page_tiles_shift = bs == 16 ? 0u : bs == 32 ? 1u : bs == 64 ? 2u : 3u;
+    p.chunk_shift = plan.shift;
+    const std::uint32_t g = p.q_group;
+    for (std::uint32_t first = 0; first < g; first += plan.sub) {
+        p.q_first = first;
+        int status = KVFLUX_OK;
+        switch (plan.sub) {
+        case 1: status = launch_bs16<E, kD, 1>(p, plan, s); break;
+        case 2: status = launch_bs16<E, kD, 2>(p, plan, s); break;
+        case 3: status = launch_bs16<E, kD, 3>(p, plan, s); break;
+        case 4: status = launch_bs16<E, kD, 4>(p, plan, s); break;
+        case 5: status = launch_bs16<E, kD, 5>(p, plan, s); break;
+        case 6: status = launch_bs16<E, kD, 6>(p, plan, s); break;
+        case 7: status = launch_bs16<E, kD, 7>(p, plan, s); break;
+        default: status = launch_bs16<E, kD, 8>(p, plan, s); break;
         }
+        if (status != KVFLUX_OK) return status;
     }
+    if (p.max_chunks > 1) return launch_combine(p, kD, 1u << plan.shift, s);
     return KVFLUX_OK;
 }
 
 template <typename E, int kD>
-int dispatch_group(Params p, std::uint64_t rows, std::uint64_t group, std::uint64_t max_chunks,
-                   hipStream_t s) {
-    if constexpr (!std::is_same<E, F32>::value && (kD == 64 || kD == 128)) {
-        // The kernel counts work items in 32 bits (at most 512-token chunks);
-        // rows <= kPlanRows keeps the product below 2^51.
-        const std::uint32_t bs = p.block_size.divisor;
-        if ((bs == 16 || bs == 32 || bs == 64 || bs == 128) && rows <= kPlanRows && p.width > 0 &&
-            rows * max_chunks * p.heads <= 0xffffffffULL) {
-            // A group above 8 runs as launches of a sub-group: the largest
-            // divisor of the group up to 8, each launch serving its slice of
-            // the query heads (and reading K/V again); the chunk partials of
-            // all of them are combined once, after the last. Group 8 at
-            // kD = 128 takes 251 VGPRs (no spills, two workgroups per CU):
-            // 1.27 against 3.10 ms on the VALU split kernel for 128 rows of
-            // U[1024, 32768] tokens with 64 query / 8 kv heads.
-            p.page_tiles_shift = bs == 16 ? 0u : bs == 32 ? 1u : bs == 64 ? 2u : 3u;
-            const auto g = static_cast<std::uint32_t>(group);
-            std::uint32_t sub = g < 8 ? g : 8;
-            while (g % sub != 0) --sub;
-            p.q_group = g;
-            for (std::uint32_t first = 0; first < g; first += sub) {
-                p.q_first = first;
-                const bool last = first + sub >= g;
-                int status = KVFLUX_OK;
-                switch (sub) {
-                case 1: status = launch_bs16<E, kD, 1>(p, max_chunks, s, last); break;
-                case 2: status = launch_bs16<E, kD, 2>(p, max_chunks, s, last); break;
-                case 3: status = launch_bs16<E, kD, 3>(p, max_chunks, s, last); break;
-                case 4: status = launch_bs16<E, kD, 4>(p, max_chunks, s, last); break;
-                case 5: status = launch_bs16<E, kD, 5>(p, max_chunks, s, last); break;
-                case 6: status = launch_bs16<E, kD, 6>(p, max_chunks, s, last); break;
-                case 7: status = launch_bs16<E, kD, 7>(p, max_chunks, s, last); break;
-                default: status = launch_bs16<E, kD, 8>(p, max_chunks, s, last); break;
-                }
-                if (status != KVFLUX_OK) return status;
-            }
-            return KVFLUX_OK;
-        }
-    }
+int run_split(Params p, std::uint64_t rows, std::uint64_t group, hipStream_t s) {
     switch (group) {
-    case 1: return launch_split<E, kD, 1>(p, rows, max_chunks, s);
-    case 2: return launch_split<E, kD, 2>(p, rows, max_chunks, s);
-    case 4: return launch_split<E, kD, 4>(p, rows, max_chunks, s);
-    case 8: return launch_split<E, kD, 8>(p, rows, max_chunks, s);
-    default: return launch_generic<E>(p, rows, kD, s);
+    case 1: return launch_split<E, kD, 1>(p, rows, s);
+    case 2: return launch_split<E, kD, 2>(p, rows, s);
+    case 4: return launch_split<E, kD, 4>(p, rows, s);
+    default: return launch_split<E, kD, 8>(p, rows, s);
     }
 }
 
 template <typename E>
-int dispatch(Params p, std::uint64_t rows, std::uint64_t head_dim, std::uint64_t group,
-             std::uint64_t max_chunks, hipStream_t s) {
-    switch (head_dim) {
-    case 64: return dispatch_group<E, 64>(p, rows, group, max_chunks, s);
-    case 128: return dispatch_group<E, 128>(p, rows, group, max_chunks, s);
-    case 256:
-        if (group <= 4) return dispatch_group<E, 256>(p, rows, group, max_chunks, s);
-        return launch_generic<E>(p, rows, head_dim, s);
-    default: return launch_generic<E>(p, rows, head_dim, s);
+int run_plan(Params p, const Plan& plan, std::uint64_t rows, std::uint64_t head_dim, std::uint64_t group,
+             hipStream_t s) {
+    switch (plan.family) {
+    case Family::Bs16:
+        if constexpr (!std::is_same<E, F32>::value) {
+            if (head_dim == 64) return run_bs16<E, 64>(p, plan, s);
+            return run_bs16<E, 128>(p, plan, s);
+        }
+        break;
+    case Family::Split:
+        if (head_dim == 64) return run_split<E, 64>(p, rows, group, s);
+        if (head_dim == 128) return run_split<E, 128>(p, rows, group, s);
+        return run_split<E, 256>(p, rows, group, s);
+    case Family::Generic: break;
     }
+    return launch_generic<E>(p, rows, head_dim, s);
 }
 
 // Whether a call may write chunk partials (and so needs the workspace): the
@@ -1306,6 +1400,89 @@ bool uses_split(std::uint64_t head_dim, std::uint64_t group) {
     if (head_dim == 64 || head_dim == 128) return group >= 1;
     if (head_dim == 256) return group == 1 || group == 2 || group == 4;
     return false;
+}
+
+// Bytes of the partial arrays for `chunks` slots per (row, query head):
+// accumulators first, then (m, l) pairs, both 256-byte aligned.
+struct PartialLayout {
+    std::uint64_t acc_bytes = 0, total = 0;
+};
+
+PartialLayout partial_layout(std::uint64_t rows, std::uint64_t query_heads, std::uint64_t chunks,
+                             std::uint64_t head_size) {
+    PartialLayout out;
+    if (chunks <= 1) return out;
+    const std::uint64_t acc = rows * query_heads * chunks * head_size * sizeof(float);
+    const std::uint64_t ml = rows * query_heads * chunks * 2 * sizeof(float);
+    out.acc_bytes = (acc + 255) & ~std::uint64_t{255};
+    out.total = out.acc_bytes + ((ml + 255) & ~std::uint64_t{255});
+    return out;
+}
+
+// Argument checks shared by both entry points; fills `p` and `plan`.
+// *empty = true when there is nothing to do (no rows).
+int prepare(const void* key_cache, const void* value_cache, uint64_t num_blocks, uint64_t num_kv_heads,
+            uint64_t block_size, uint64_t head_size, int dtype, const uint64_t* block_table,
+            uint64_t max_blocks_per_seq, const uint64_t* seq_lens, uint64_t kv_len, uint64_t num_rows,
+            uint64_t query_heads, const float* query, float* output, Params* p, Plan* plan) {
+    if (dtype_bytes(dtype) == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+    if (!key_cache || !value_cache || !block_table || !query || !output) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged attention: null pointer");
+    }
+    if (num_blocks == 0 || num_kv_heads == 0 || block_size == 0 || head_size == 0 ||
+        query_heads == 0 || query_heads % num_kv_heads != 0) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged attention: invalid shape");
+    }
+    if (!seq_lens && num_rows > kv_len) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged attention: more queries than tokens");
+    }
+    if (num_rows > 0xffffffffULL || query_heads > 0xffffffffULL || num_kv_heads > 65535 ||
+        block_size > 0xffffffffULL || kv_len > 0xffffffffULL) {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: dimension too large");
+    }
+    const std::uint64_t group = query_heads / num_kv_heads;
+    if (!uses_split(head_size, group) && head_size > kGenericMaxD) {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: head_size %llu > %d",
+                    static_cast<unsigned long long>(head_size), kGenericMaxD);
+    }
+    const std::uint64_t max_chunks = (kv_len + kChunk - 1) / kChunk;
+    *p = Params{};
+    p->key_cache = key_cache;
+    p->value_cache = value_cache;
+    p->num_blocks = num_blocks;
+    p->heads = static_cast<std::uint32_t>(num_kv_heads);
+    p->block_size = FastDiv(static_cast<std::uint32_t>(block_size));
+    p->table = block_table;
+    p->width = max_blocks_per_seq;
+    p->seq_lens = seq_lens;
+    p->kv_len = kv_len;
+    p->num_rows = static_cast<std::uint32_t>(num_rows);
+    p->query_heads = static_cast<std::uint32_t>(query_heads);
+    p->query = query;
+    p->output = output;
+    p->q_group = static_cast<std::uint32_t>(group);
+    p->q_first = 0;
+    p->scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_size)));
+    int status = KVFLUX_OK;
+    switch (dtype) {
+    case KVFLUX_DTYPE_BF16: status = plan_call<Bf16>(*p, num_rows, head_size, group, max_chunks, plan); break;
+    case KVFLUX_DTYPE_F16: status = plan_call<F16>(*p, num_rows, head_size, group, max_chunks, plan); break;
+    default: status = plan_call<F32>(*p, num_rows, head_size, group, max_chunks, plan); break;
+    }
+    if (status != KVFLUX_OK) return status;
+    // The partial arrays' stride; 1 (or 0) tells the kernels that no
+    // partials are written.
+    p->max_chunks = static_cast<std::uint32_t>(plan->chunks);
+    return KVFLUX_OK;
+}
+
+int launch_prepared(Params p, const Plan& plan, int dtype, std::uint64_t head_size, hipStream_t s) {
+    const std::uint64_t group = p.q_group;
+    switch (dtype) {
+    case KVFLUX_DTYPE_BF16: return run_plan<Bf16>(p, plan, p.num_rows, head_size, group, s);
+    case KVFLUX_DTYPE_F16: return run_plan<F16>(p, plan, p.num_rows, head_size, group, s);
+    default: return run_plan<F32>(p, plan, p.num_rows, head_size, group, s);
+    }
 }
 
 } // namespace
@@ -1331,10 +1508,7 @@ extern "C" int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t
     if (need > static_cast<long double>(~std::size_t{0} / 2)) {
         return fail(KVFLUX_ERR_OVERFLOW, "attention workspace size overflow");
     }
-    // Accumulators first, then (m, l) pairs; both 256-byte aligned.
-    const std::uint64_t acc = num_rows * query_heads * chunks * head_size * sizeof(float);
-    const std::uint64_t ml = num_rows * query_heads * chunks * 2 * sizeof(float);
-    *bytes = ((acc + 255) & ~std::uint64_t{255}) + ((ml + 255) & ~std::uint64_t{255});
+    *bytes = partial_layout(num_rows, query_heads, chunks, head_size).total;
     return KVFLUX_OK;
 }
 
@@ -1346,62 +1520,24 @@ extern "C" int kvflux_paged_attention(const void* key_cache, const void* value_c
                                       uint64_t query_heads, const float* query, float* output,
                                       void* workspace, size_t workspace_bytes, void* stream) {
     if (num_rows == 0) return KVFLUX_OK;
-    if (dtype_bytes(dtype) == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
-    if (!key_cache || !value_cache || !block_table || !query || !output) {
-        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged attention: null pointer");
-    }
-    if (num_blocks == 0 || num_kv_heads == 0 || block_size == 0 || head_size == 0 ||
-        query_heads == 0 || query_heads % num_kv_heads != 0) {
-        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged attention: invalid shape");
-    }
-    if (!seq_lens && num_rows > kv_len) {
-        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged attention: more queries than tokens");
-    }
-    if (num_rows > 0xffffffffULL || query_heads > 0xffffffffULL || num_kv_heads > 65535 ||
-        block_size > 0xffffffffULL || kv_len > 0xffffffffULL) {
-        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: dimension too large");
-    }
-    const std::uint64_t group = query_heads / num_kv_heads;
-    if (!uses_split(head_size, group) && head_size > kGenericMaxD) {
-        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: head_size %llu > %d",
-                    static_cast<unsigned long long>(head_size), kGenericMaxD);
-    }
+    Params p;
+    Plan plan;
+    int status = prepare(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype,
+                         block_table, max_blocks_per_seq, seq_lens, kv_len, num_rows, query_heads, query,
+                         output, &p, &plan);
+    if (status != KVFLUX_OK) return status;
+    // The documented size (partials of 512-token items) bounds every plan.
     std::size_t need = 0;
-    int status = kvflux_paged_attention_workspace_size(num_rows, kv_len, num_kv_heads, query_heads,
-                                                       block_size, head_size, &need);
+    status = kvflux_paged_attention_workspace_size(num_rows, kv_len, num_kv_heads, query_heads, block_size,
+                                                   head_size, &need);
     if (status != KVFLUX_OK) return status;
     if (need > 0 && (!workspace || workspace_bytes < need)) {
         return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged attention: workspace needs %zu bytes", need);
     }
-    const std::uint64_t chunks = (kv_len + kChunk - 1) / kChunk;
-    Params p{};
-    p.key_cache = key_cache;
-    p.value_cache = value_cache;
-    p.num_blocks = num_blocks;
-    p.heads = static_cast<std::uint32_t>(num_kv_heads);
-    p.block_size = FastDiv(static_cast<std::uint32_t>(block_size));
-    p.table = block_table;
-    p.width = max_blocks_per_seq;
-    p.seq_lens = seq_lens;
-    p.kv_len = kv_len;
-    p.num_rows = static_cast<std::uint32_t>(num_rows);
-    p.query_heads = static_cast<std::uint32_t>(query_heads);
-    p.query = query;
-    p.output = output;
-    p.max_chunks = static_cast<std::uint32_t>(chunks);
-    p.q_group = static_cast<std::uint32_t>(group);
-    p.q_first = 0;
-    p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_size)));
-    if (need > 0) {
-        const std::uint64_t acc = num_rows * query_heads * chunks * head_size * sizeof(float);
+    const PartialLayout layout = partial_layout(num_rows, query_heads, plan.chunks, head_size);
+    if (layout.total > 0) {
         p.partial_acc = static_cast<float*>(workspace);
-        p.partial_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                ((acc + 255) & ~std::uint64_t{255}));
+        p.partial_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + layout.acc_bytes);
     }
-    const hipStream_t s = as_stream(stream);
-    switch (dtype) {
-    case KVFLUX_DTYPE_BF16: return dispatch<Bf16>(p, num_rows, head_size, group, chunks, s);
-    case KVFLUX_DTYPE_F16: return dispatch<F16>(p, num_rows, head_size, group, chunks, s);
-    default: return dispatch<F32>(p, num_rows, head_size, group, chunks, s);
-    }
+    return launch_prepared(p, plan, dtype, head_size, as_stream(stream));
 }
