@@ -156,6 +156,27 @@ int kvflux_paged_attention(const void* key_cache, const void* value_cache,
                            const float* query, float* output, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* kvflux_paged_attention_noalloc: kvflux_paged_attention without a workspace
+ * argument and without any device allocation, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc, harnesses with a fixed memory budget). No counterpart in the
+ * reference, whose paged_attention_batch allocates its metadata per call
+ * (src/v2/paged_attention.cu:287-292). Same kernels, same results (bit for
+ * bit) as kvflux_paged_attention. The chunk partials live in a static device
+ * array of KVFLUX_NOALLOC_SCRATCH_BYTES that each device holds until the
+ * process ends; a call whose partials exceed it fails with
+ * KVFLUX_ERR_UNSUPPORTED (at the 128-row, 32K-token, 32 q-head, head_size 128
+ * decode batch the partials take 17 MB). All calls on one device share that
+ * array: calls that overlap on one device (different streams, or threads)
+ * race and must be serialised by the caller. */
+#define KVFLUX_NOALLOC_SCRATCH_BYTES (32ull << 20)
+int kvflux_paged_attention_noalloc(const void* key_cache, const void* value_cache,
+                                   uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
+                                   uint64_t head_size, int dtype, const uint64_t* block_table,
+                                   uint64_t max_blocks_per_seq, const uint64_t* seq_lens,
+                                   uint64_t kv_len, uint64_t num_rows, uint64_t query_heads,
+                                   const float* query, float* output, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Hot path 3b: causal paged prefill on MFMA (BF16/FP16 caches only).
  * Replaces paged_attention_kernel for a whole-prompt call

@@ -56,6 +56,8 @@ SIGNATURES = {
                                                      C.POINTER(C.c_size_t)]),
     "kvflux_paged_attention": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _vp,
                                       _u64, _u64, _u64, _vp, _vp, _vp, _sz, _vp]),
+    "kvflux_paged_attention_noalloc": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _vp,
+                                              _u64, _u64, _u64, _vp, _vp, _vp]),
     "kvflux_paged_prefill": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _u64,
                                     _u64, _u64, _vp, _vp, _vp]),
     "kvflux_paged_prefill_workspace_size": (_i32, [_u64, _u64, _u64, _u64, _u64, C.POINTER(_sz)]),

@@ -27,6 +27,7 @@
 #include "common.h"
 
 #include <atomic>
+#include <mutex>
 #include <cmath>
 #include <type_traits>
 
@@ -1538,6 +1539,86 @@ extern "C" int kvflux_paged_attention(const void* key_cache, const void* value_c
     if (layout.total > 0) {
         p.partial_acc = static_cast<float*>(workspace);
         p.partial_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + layout.acc_bytes);
+    }
+    return launch_prepared(p, plan, dtype, head_size, as_stream(stream));
+}
+
+// ---------------------------------------------------------------- no-allocation entry
+//
+// kvflux_paged_attention_noalloc runs the same plan as kvflux_paged_attention
+// with the chunk partials in `scratch`, a file-scope device array of
+// KVFLUX_NOALLOC_SCRATCH_BYTES that every device holds from module load until
+// the process ends. Host code never passes the array's name to a kernel: its
+// device address comes from hipGetSymbolAddress, taken once per device (with
+// that device current) at the first call there and kept in scratch_base.
+// Every call on one device shares that device's array (its contents are
+// whatever the last call left; the kernels need no initialisation), so calls
+// that overlap on one device race.
+namespace kvflux_hip {
+
+__device__ __attribute__((aligned(256))) unsigned char scratch[KVFLUX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex scratch_mutex;
+void* scratch_base[kMaxDevices] = {};
+
+// Device address of the current device's copy of `scratch`.
+int scratch_address(void** out) {
+    int device = 0;
+    int status = hip_status(hipGetDevice(&device), "hipGetDevice");
+    if (status != KVFLUX_OK) return status;
+    const bool cached = device >= 0 && device < kMaxDevices;
+    if (cached) {
+        std::lock_guard<std::mutex> lock(scratch_mutex);
+        if (scratch_base[device]) {
+            *out = scratch_base[device];
+            return KVFLUX_OK;
+        }
+    }
+    void* ptr = nullptr;
+    status = hip_status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress");
+    if (status != KVFLUX_OK) return status;
+    if (!ptr) return fail(KVFLUX_ERR_RUNTIME, "hipGetSymbolAddress returned no address for the scratch array");
+    if (cached) {
+        std::lock_guard<std::mutex> lock(scratch_mutex);
+        scratch_base[device] = ptr;
+    }
+    *out = ptr;
+    return KVFLUX_OK;
+}
+
+} // namespace
+} // namespace kvflux_hip
+
+extern "C" int kvflux_paged_attention_noalloc(const void* key_cache, const void* value_cache,
+                                              uint64_t num_blocks, uint64_t num_kv_heads,
+                                              uint64_t block_size, uint64_t head_size, int dtype,
+                                              const uint64_t* block_table, uint64_t max_blocks_per_seq,
+                                              const uint64_t* seq_lens, uint64_t kv_len, uint64_t num_rows,
+                                              uint64_t query_heads, const float* query, float* output,
+                                              void* stream) {
+    if (num_rows == 0) return KVFLUX_OK;
+    Params p;
+    Plan plan;
+    int status = prepare(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype,
+                         block_table, max_blocks_per_seq, seq_lens, kv_len, num_rows, query_heads, query,
+                         output, &p, &plan);
+    if (status != KVFLUX_OK) return status;
+    const PartialLayout layout = partial_layout(num_rows, query_heads, plan.chunks, head_size);
+    if (layout.total > KVFLUX_NOALLOC_SCRATCH_BYTES) {
+        return fail(KVFLUX_ERR_UNSUPPORTED,
+                    "paged attention (no allocation): this call needs %llu bytes of chunk partials, "
+                    "more than the %llu-byte static scratch; use kvflux_paged_attention with a workspace",
+                    static_cast<unsigned long long>(layout.total),
+                    static_cast<unsigned long long>(KVFLUX_NOALLOC_SCRATCH_BYTES));
+    }
+    if (layout.total > 0) {
+        void* base = nullptr;
+        status = scratch_address(&base);
+        if (status != KVFLUX_OK) return status;
+        p.partial_acc = static_cast<float*>(base);
+        p.partial_ml = reinterpret_cast<float*>(static_cast<char*>(base) + layout.acc_bytes);
     }
     return launch_prepared(p, plan, dtype, head_size, as_stream(stream));
 }
