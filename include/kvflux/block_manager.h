@@ -1,36 +1,22 @@
 #pragma once
-// Page-id allocator underneath PhysicalBlockPool.
-// Same public surface as the reference's include/kvflux/block_manager.h:14-78:
-// LIFO reuse of freed ids (ids are handed out 0,1,2,... on a fresh manager and
-// the most recently freed id comes back first), per-id reference counts,
-// generation-checked handles, and publish/lookup of full-block token prefixes
-// with a zero-reference LRU that allocate() evicts from when no id is free.
-// Single-threaded: callers serialise access.
+// v0 page-id allocator. Same public surface as the reference's
+// include/kvflux/block_manager.h:14-78: LIFO reuse of freed ids (ids are
+// handed out 0, 1, 2, ... on a fresh manager and the most recently freed id
+// comes back first), per-id reference counts, generation-checked handles,
+// and publish/lookup of full-block token prefixes with eviction of the least
+// recently idled published page when no id is free. Page state lives in a
+// detail::PageLedger (include/kvflux/detail/page_ledger.h); this class adds
+// the v0 whole-sequence table helpers. Single-threaded: callers serialise
+// access.
 
-#include "kvflux/detail/index_lru.h"
+#include "kvflux/detail/page_ledger.h"
 
 #include <cstddef>
 #include <cstdint>
 #include <functional>
-#include <stdexcept>
-#include <unordered_map>
 #include <vector>
 
 namespace kvflux {
-
-using Token = std::int32_t;
-using Tokens = std::vector<Token>;
-
-// `id` names a page; `generation` distinguishes successive lifetimes of that
-// page so a handle kept past its last release is rejected.
-struct BlockHandle {
-    std::size_t id;
-    std::uint64_t generation;
-    bool operator==(const BlockHandle& other) const noexcept {
-        return id == other.id && generation == other.generation;
-    }
-    bool operator!=(const BlockHandle& other) const noexcept { return !(*this == other); }
-};
 
 // v0 per-sequence table used by BlockManager::acquire/share/release.
 // Copying the struct does not take references.
@@ -39,15 +25,9 @@ struct BlockTable {
     std::size_t token_count = 0;
 };
 
-// Thrown when every page is referenced and none can be evicted.
-class CapacityError : public std::runtime_error {
-public:
-    CapacityError() : std::runtime_error("no reclaimable KV block") {}
-};
-
 class BlockManager {
 public:
-    using Hasher = std::function<std::uint64_t(const Tokens&)>;
+    using Hasher = detail::PageLedger::Hasher;
     struct Stats {
         std::size_t capacity, free, active, cached_idle;
     };
@@ -60,22 +40,17 @@ public:
     BlockManager& operator=(BlockManager&&) = delete;
 
     // One reference per allocate/retain; release each exactly once.
-    BlockHandle allocate();
-    void retain(BlockHandle handle);
-    void release(BlockHandle handle);
-    std::size_t ref_count(BlockHandle handle) const;
-    bool is_published(BlockHandle handle) const;
-    // Page ids of n handles that each hold a reference, checked as
-    // ref_count does (std::invalid_argument for a stale handle, or one with no
-    // reference); out[i] = handles[i].id. One pass, for building tables.
-    // No counterpart in the reference.
-    void referenced_ids(const BlockHandle* handles, std::size_t n, std::size_t* out) const;
+    BlockHandle allocate() { return ledger_.take(); }
+    void retain(BlockHandle handle) { ledger_.hold(handle); }
+    void release(BlockHandle handle) { ledger_.drop(handle); }
+    std::size_t ref_count(BlockHandle handle) const { return ledger_.holders(handle); }
+    bool is_published(BlockHandle handle) const { return ledger_.published(handle); }
 
     // Index a privately held full block under the tokens from the start of
     // the sequence to the end of that block.
-    void publish(BlockHandle handle, const Tokens& prefix);
+    void publish(BlockHandle handle, const Tokens& prefix) { ledger_.publish(handle, prefix); }
     // On a hit, takes one reference and writes the handle to `out`.
-    bool lookup(const Tokens& prefix, BlockHandle& out);
+    bool lookup(const Tokens& prefix, BlockHandle& out) { return ledger_.find(prefix, out); }
 
     // Whole-sequence helpers of the v0 API: full blocks are looked up or
     // published automatically, a partial tail block stays private.
@@ -85,32 +60,15 @@ public:
     BlockHandle block_at(const BlockTable& table, std::size_t token_index) const;
 
     Stats stats() const noexcept;
-    std::size_t capacity() const noexcept { return pages_.size(); }
-    std::size_t block_size() const noexcept { return block_size_; }
+    std::size_t capacity() const noexcept { return ledger_.capacity(); }
+    std::size_t block_size() const noexcept { return ledger_.block_size(); }
     // 64-bit FNV-1a over each token's four little-endian bytes.
     static std::uint64_t prefix_hash(const Tokens& prefix) noexcept;
 
 private:
-    struct Page {
-        std::uint64_t generation = 0;
-        std::size_t refs = 0;
-        bool in_use = false;   // false: sitting in the free stack
-        bool published = false;
-        std::uint64_t hash = 0;
-        Tokens prefix;
-    };
-    const Page& live(BlockHandle handle) const;
-    Page& live(BlockHandle handle);
-    void unpublish(std::size_t id);
     void check_table(const BlockTable& table) const;
 
-    std::vector<Page> pages_;
-    std::vector<std::size_t> free_stack_;  // top = back(); next id to hand out
-    std::size_t block_size_;
-    Hasher hasher_;
-    detail::IndexLru idle_;                // published pages with refs == 0
-    std::size_t idle_count_ = 0;
-    std::unordered_map<std::uint64_t, std::vector<std::size_t>> by_hash_;
+    detail::PageLedger ledger_;
 };
 
 } // namespace kvflux

@@ -1,7 +1,8 @@
 #pragma once
 // Owner of physical page ids for the paged KV cache (metadata only; it holds
 // no device memory). Same surface as the reference's
-// include/kvflux/physical_block_pool.h:22-58; backed by BlockManager.
+// include/kvflux/physical_block_pool.h:22-58. Page state lives in a
+// detail::PageLedger, the same ledger BlockManager uses.
 
 #include "kvflux/block_manager.h"
 
@@ -45,7 +46,7 @@ public:
     std::size_t available() const noexcept;
 
 private:
-    BlockManager manager_;
+    detail::PageLedger ledger_;
 };
 
 } // namespace kvflux

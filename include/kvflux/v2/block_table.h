@@ -11,6 +11,8 @@
 
 namespace kvflux::v2 {
 
+class SequenceState;
+
 class BlockTable {
 public:
     explicit BlockTable(PhysicalBlockPool& pool) noexcept;
@@ -53,6 +55,14 @@ public:
     void clear() noexcept;
 
 private:
+    friend class SequenceState;
+    // Makes room for `n` more entries (geometric growth), so that a later
+    // adopt() of n handles cannot fail.
+    void make_room(std::size_t n);
+    // Appends handles whose references the caller hands over; room for them
+    // was made first.
+    void adopt(const std::vector<PhysicalBlockHandle>& handles) noexcept;
+
     PhysicalBlockPool* pool_;  // nullptr after being moved from
     std::vector<PhysicalBlockHandle> entries_;
 };

@@ -12,17 +12,21 @@ namespace kvflux::v2 {
 
 // Arithmetic contract of an attention call.
 //   Exact: FP32 Q and FP32 accumulation of every product; matches the
-//          double-precision CPU reference to ~1e-6 for any KV dtype.
-//   Auto:  Exact, except that 16-bit KV caches with head_size 64 or 128 and
-//          query_tokens >= 16 use the MFMA prefill kernel, where Q and the
-//          softmax weights are rounded to the cache dtype (2e-2 contract).
-//   Fast:  MFMA prefill whenever the shape allows it (16-bit KV,
-//          head_size 64/128), otherwise Exact.
+//          double-precision CPU reference to ~1e-6 for any KV dtype (the
+//          reference's 1e-5 contract). The reference's own signature below
+//          uses it.
+//   Auto:  Exact, except that calls of query_tokens >= 16 on the shapes the
+//          MFMA prefill takes (16-bit KV cache, head_size 64, 128 or 256,
+//          block_size a power of two up to 256) run there: Q and the softmax
+//          weights are rounded to the cache dtype (2e-2 contract).
+//   Fast:  the MFMA prefill whenever the shape allows it (any query_tokens),
+//          otherwise Exact.
 enum class AttentionPrecision { Exact, Auto, Fast };
 
 // Single request: Q/O are device FP32 [query_tokens][query_heads][head_size];
 // query i sees cache positions <= num_tokens - query_tokens + i.
-// Uses AttentionPrecision::Auto.
+// Uses AttentionPrecision::Exact, the reference's contract; pass Auto or Fast
+// to the overload below for the MFMA prefill.
 void paged_attention(const PagedKVStorage& storage, const SequenceState& sequence,
                      const float* query_device, float* output_device,
                      std::size_t query_tokens, std::size_t query_heads);

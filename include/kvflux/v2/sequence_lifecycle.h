@@ -2,6 +2,7 @@
 // Synchronous single-request prefill/decode driver over the paged data path.
 // Same surface as the reference's include/kvflux/v2/sequence_lifecycle.h:12-47.
 
+#include "kvflux/v2/paged_attention.h"
 #include "kvflux/v2/paged_kv_storage.h"
 
 #include <cstddef>
@@ -11,8 +12,10 @@ namespace kvflux::v2 {
 
 class SequenceLifecycle {
 public:
+    // `precision` (an addition to the reference's constructor) selects the
+    // attention contract of prefill and decode; Exact is the reference's.
     SequenceLifecycle(RequestID request_id, PhysicalBlockPool& pool, PagedKVStorage& storage,
-                      std::size_t query_heads);
+                      std::size_t query_heads, AttentionPrecision precision = AttentionPrecision::Exact);
     ~SequenceLifecycle() noexcept { finish(); }
     SequenceLifecycle(const SequenceLifecycle&) = delete;
     SequenceLifecycle& operator=(const SequenceLifecycle&) = delete;
@@ -34,11 +37,16 @@ public:
     const SequenceState& sequence() const;
 
 private:
+    // Runs one step; on any exception waits for the device, finishes the
+    // request (its pages go back) and rethrows.
+    template <typename Step>
+    auto guarded(Step&& step) -> decltype(step());
     void abort_after_failure() noexcept;
 
     PagedKVStorage& storage_;
     std::optional<SequenceState> sequence_;
     std::size_t query_heads_;
+    AttentionPrecision precision_;
     bool prefilled_ = false;
 };
 

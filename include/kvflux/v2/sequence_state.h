@@ -60,8 +60,14 @@ public:
 private:
     friend class PrefixCache;
     friend struct detail::SequenceAccess;
-    void append_cached_full_block(PhysicalBlockHandle handle);
+    // Room for `n` more table entries (std::bad_alloc is the only failure).
+    void reserve_blocks(std::size_t n);
+    // Maps whole published blocks onto an empty sequence: `handles` carry one
+    // reference each, which the table takes over; room was reserved first.
+    void adopt_cached_blocks(const std::vector<PhysicalBlockHandle>& handles) noexcept;
     PhysicalBlockHandle block_handle(std::size_t logical_block) const;
+    // The tail page is partially filled and shared with another holder.
+    bool tail_shared_and_partial() const;
 
     RequestID id_;
     std::size_t tokens_ = 0;

@@ -12,9 +12,11 @@
 #include <chrono>
 #include <cstddef>
 #include <cstdint>
+#include <deque>
 #include <optional>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 namespace kvflux::v3 {
 
@@ -75,7 +77,7 @@ public:
     bool contains(const CacheKey& key) const;
     // std::out_of_range for an unknown key (every call below too).
     const ChunkRecord& at(const CacheKey& key) const;
-    std::size_t size() const noexcept { return records_.size(); }
+    std::size_t size() const noexcept { return index_.size(); }
 
     // Allocates a slot on `tier` and records a replica there.
     // std::logic_error if the tier already holds one; CapacityError if full.
@@ -110,12 +112,19 @@ public:
     void destroy(const CacheKey& key);
 
 private:
-    ChunkRecord& lookup(const CacheKey& key);
-    static std::optional<Replica>& replica_of(ChunkRecord& record, StorageTier tier);
-    static const std::optional<Replica>& replica_of(const ChunkRecord& record, StorageTier tier);
+    // Records live in a slab whose addresses never move (at() hands out
+    // references); destroyed records leave a vacant entry for the next
+    // create(). The index maps a key to its slab entry.
+    ChunkRecord& record(const CacheKey& key);
+    // Position of `tier` in tiers_ / replicas_ (std::invalid_argument for a
+    // value outside the enum).
+    static std::size_t tier_index(StorageTier tier);
 
-    Tier* tiers_[3];  // indexed by StorageTier
-    std::unordered_map<CacheKey, ChunkRecord, CacheKeyHash> records_;
+    Tier* tiers_[3];                 // indexed by StorageTier
+    std::size_t replicas_[3] = {};   // records holding a replica on each tier
+    std::deque<ChunkRecord> slab_;
+    std::vector<std::size_t> vacant_;
+    std::unordered_map<CacheKey, std::size_t, CacheKeyHash> index_;
 };
 
 } // namespace kvflux::v3

@@ -6,6 +6,7 @@
 #include "kvflux/v3/tier.h"
 
 #include <cstddef>
+#include <memory>
 #include <vector>
 
 namespace kvflux::v3 {
@@ -35,7 +36,7 @@ public:
 private:
     std::size_t slots_;
     std::size_t chunk_bytes_;
-    std::vector<unsigned char> bytes_;
+    std::unique_ptr<unsigned char[]> bytes_;  // slots * chunk_bytes, zero-filled
 };
 
 } // namespace kvflux::v3

@@ -396,8 +396,9 @@ PYBIND11_MODULE(_kvflux, m) {
     });
 
     py::class_<SequenceLifecycle>(m, "SequenceLifecycle")
-        .def(py::init<RequestID, PhysicalBlockPool&, PagedKVStorage&, std::size_t>(),
-             py::keep_alive<1, 3>(), py::keep_alive<1, 4>())
+        .def(py::init<RequestID, PhysicalBlockPool&, PagedKVStorage&, std::size_t, AttentionPrecision>(),
+             py::arg("request_id"), py::arg("pool"), py::arg("storage"), py::arg("query_heads"),
+             py::arg("precision") = AttentionPrecision::Exact, py::keep_alive<1, 3>(), py::keep_alive<1, 4>())
         .def("prefill", [](SequenceLifecycle& s, std::size_t n, std::uintptr_t k, std::uintptr_t v,
                            std::uintptr_t q, std::uintptr_t o) {
             py::gil_scoped_release release;
@@ -436,7 +437,7 @@ PYBIND11_MODULE(_kvflux, m) {
                         query_tokens, query_heads, precision);
     }, py::arg("storage"), py::arg("sequence"), py::arg("query"), py::arg("output"),
        py::arg("query_tokens"), py::arg("query_heads"),
-       py::arg("precision") = AttentionPrecision::Auto);
+       py::arg("precision") = AttentionPrecision::Exact);
     py::class_<AttentionShape>(m, "AttentionShape")
         .def(py::init([](std::size_t qt, std::size_t kt, std::size_t qh, std::size_t kh, std::size_t d) {
                  return AttentionShape{qt, kt, qh, kh, d};

@@ -193,7 +193,7 @@ void paged_attention(const PagedKVStorage& storage, const SequenceState& sequenc
                      const float* query_device, float* output_device,
                      std::size_t query_tokens, std::size_t query_heads) {
     paged_attention(storage, sequence, query_device, output_device, query_tokens, query_heads,
-                    AttentionPrecision::Auto);
+                    AttentionPrecision::Exact);
 }
 
 void paged_attention(const PagedKVStorage& storage, const SequenceState& sequence,

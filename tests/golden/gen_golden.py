@@ -45,6 +45,13 @@ TRACE_CASES = [  # (seed, capacity, block_size, steps)
     (13, 8, 2, 300),
     (14, 200, 16, 800),
 ]
+# Prefix-sharing churn (trace_ops.churn_trace): small pools, long traces, so
+# idle published pages are held, released and evicted thousands of times.
+CHURN_CASES = [  # (seed, capacity, block_size, steps)
+    (21, 6, 2, 4000),
+    (22, 12, 4, 6000),
+    (23, 24, 1, 6000),
+]
 
 
 def attention_fixture() -> dict:
@@ -77,6 +84,12 @@ def trace_fixture() -> dict:
         data[f"t{seed}/config"] = np.array([capacity, block_size], np.int64)
         data[f"t{seed}/ops"] = ops
         data[f"t{seed}/results"] = results
+    for seed, capacity, block_size, steps in CHURN_CASES:
+        ops = trace_ops.churn_trace(seed, capacity, block_size, steps)
+        results = oracle.ref_run_trace(capacity, block_size, ops)
+        data[f"c{seed}/config"] = np.array([capacity, block_size], np.int64)
+        data[f"c{seed}/ops"] = ops
+        data[f"c{seed}/results"] = results
     return data
 
 

@@ -203,7 +203,8 @@ def test_prefill_through_cpp_layer(gpu, v2, kv_heads, q_heads):
 def test_precision_routing(gpu, v2):
     """Auto sends calls of 16 or more query tokens to the MFMA prefill (the
     same bits as Fast) and fewer to the exact kernels (the same bits as
-    Exact, which is within 1e-5 of the oracle)."""
+    Exact, which is within 1e-5 of the oracle). The reference's own
+    six-argument signature (no precision) is Exact at every length."""
     pool = v2.PhysicalBlockPool(64, 16)
     storage = v2.PagedKVStorage(pool, 2, 128, v2.DType.BFloat16)
     seq = v2.SequenceState(1, pool)
@@ -223,6 +224,9 @@ def test_precision_routing(gpu, v2):
             od = buffer_like(np.zeros(q.size, np.float32))
             v2.paged_attention(storage, seq, qd.ptr, od.ptr, q_tokens, 8, prec)
             out[prec] = od.download(np.float32).view(np.uint32)
+        od = buffer_like(np.zeros(q.size, np.float32))
+        v2.paged_attention(storage, seq, qd.ptr, od.ptr, q_tokens, 8)  # reference signature
+        assert np.array_equal(od.download(np.float32).view(np.uint32), out[P.Exact]), q_tokens
         twin = P.Exact if q_tokens < 16 else P.Fast
         assert np.array_equal(out[P.Auto], out[twin]), q_tokens
         exp = oracle.paged_attention_causal(kh, vh, 2, 16, 128, oracle.BF16, table, 300, q, q_tokens, 8)

@@ -61,6 +61,46 @@ def random_trace(seed: int, capacity: int, block_size: int, steps: int) -> np.nd
     return np.asarray(ops, dtype=np.int64).reshape(-1)
 
 
+def churn_trace(seed: int, capacity: int, block_size: int, steps: int) -> np.ndarray:
+    """A seeded op sequence heavy on prefix sharing: blocks are published,
+    their sequences dropped (the pages go idle), re-attached by new
+    sequences (idle pages held again) and evicted by allocations under
+    capacity pressure, thousands of times over a small pool."""
+    rng = random.Random(seed)
+    ops = []
+    seqs = []
+    nseq = 0
+    for _ in range(steps):
+        r = rng.random()
+        if r < 0.14 or not seqs:
+            ops.append((NEW_SEQ, 0, 0)); seqs.append(nseq); nseq += 1
+            if rng.random() < 0.7:  # attach a cached prefix to the new, empty sequence
+                ops.append((ATTACH, nseq - 1, rng.choice([block_size, 2 * block_size, 3 * block_size,
+                                                          4 * block_size + 1])))
+        elif r < 0.34:
+            s = rng.choice(seqs)
+            ops.append((APPEND, s, rng.choice([1, block_size - 1, block_size, 2 * block_size])))
+        elif r < 0.52:
+            ops.append((PUBLISH, rng.choice(seqs), rng.randrange(0, 4)))
+        elif r < 0.70 and len(seqs) > 1:
+            s = rng.choice(seqs); seqs.remove(s); ops.append((DROP, s, 0))
+        elif r < 0.76:
+            ops.append((AVAILABLE, 0, 0))
+        elif r < 0.84:
+            ops.append((TABLE, rng.choice(seqs), 0))
+        elif r < 0.90:
+            ops.append((APPEND_ONE, rng.choice(seqs), 0))
+        elif r < 0.93:
+            ops.append((FORK, rng.choice(seqs), 0)); seqs.append(nseq); nseq += 1
+        elif r < 0.97:
+            ops.append((REFS, rng.choice(seqs), rng.randrange(0, 4)))
+        else:
+            ops.append((APPEND_COW, rng.choice(seqs), 0))
+        if len(seqs) > 8:  # keep the live set small so the pool churns
+            s = seqs.pop(0); ops.append((DROP, s, 0))
+    return np.asarray(ops, dtype=np.int64).reshape(-1)
+
+
 def _status(exc: BaseException, v2) -> int:
     if isinstance(exc, v2.CapacityError):
         return -4
