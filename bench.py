@@ -618,27 +618,121 @@ def bench_prefill(v2, args, stream):
                                        [out.ptr + i * T * Hq * D * 4 for i in range(S)], Hq,
                                        v2.AttentionPrecision.Fast, 3) * 1e3
     flops = S * T * (T + 1) / 2 * Hq * D * 4
-    # The last queries (longest rows) of the first and last sequence against the CPU reference.
+    # 16 rows of every sequence (first and last tokens, tile and page
+    # boundaries, a seeded sample) against the CPU reference.
     page_bytes = H * bs * D * 2
     err = 0.0
     checked = 0
-    for i in (0, S - 1):
+    local = np.arange(npages, dtype=np.uint64)
+    for i in range(S):
         ids = device.memcpy_d2h(tables[i].ptr, npages * 8, np.uint64)
         kc = np.concatenate([device.memcpy_d2h(kb + int(p) * page_bytes, page_bytes, np.uint16) for p in ids])
         vc = np.concatenate([device.memcpy_d2h(vb + int(p) * page_bytes, page_bytes, np.uint16) for p in ids])
-        tail = 2
-        qh = device.memcpy_d2h(qs[i].ptr + (T - tail) * Hq * D * 4, tail * Hq * D * 4, np.float32)
-        ref = oracle.paged_attention_causal(kc, vc, H, bs, D, oracle.BF16, np.arange(npages, dtype=np.uint64), T, qh,
-                                            tail, Hq, threads=8)
-        got = device.memcpy_d2h(out.ptr + (i * T + T - tail) * Hq * D * 4, tail * Hq * D * 4, np.float32)
-        err = max(err, float(np.abs(got - ref).max()))
-        checked += tail
+        rows = sorted({0, 63, 64, 1000, 2047, 2048, 4094, 4095} | set(rng.integers(0, T, 8).tolist()))
+        qall = device.memcpy_d2h(qs[i].ptr, T * Hq * D * 4, np.float32).reshape(T, Hq * D)
+        oall = device.memcpy_d2h(out.ptr + i * T * Hq * D * 4, T * Hq * D * 4, np.float32).reshape(T, Hq * D)
+        ref = oracle.paged_attention_rows(kc, vc, H, bs, D, oracle.BF16, np.tile(local, len(rows)), npages,
+                                          np.array([t + 1 for t in rows], np.uint64), qall[rows].reshape(-1), Hq,
+                                          threads=8)
+        err = max(err, float(np.abs(oall[rows].reshape(-1) - ref).max()))
+        checked += len(rows)
     del seqs
     tflops = flops / (ms * 1e-3) / 1e12
     return {"workload": "8 x 4096-token causal prefill, 32 q / 8 kv heads, D=128, BF16 KV, block_size 16",
             "kernel": "paged_prefill_kernel<bf16,128,4>", "ms": ms, "api_ms": api_ms, "TFLOPs": tflops,
             "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS, "flops": flops,
             "max_abs_err_vs_oracle": err, "rows_checked": checked, "tolerance": 2e-2}
+
+
+def bench_ceilings(v2, args, stream):
+    """Bandwidth ceilings of this part for the gather's traffic, all with
+    committed kernels on 2.32 GB (the gather configuration's bytes):
+      gather_fragmented : the gather configuration (odd pages, BF16)
+      gather_contiguous : the same kernel on an identity table of whole
+                          pages, i.e. a plain copy of the same bytes
+      memcpy_d2d        : the runtime's device-to-device copy (read + write)
+      write_only        : kvflux_fill_bytes
+      read_only         : kvflux_compare_bytes of two halves (synchronous:
+                          one counter upload and readback included)"""
+    from kvflux_amd import capi, device
+
+    out = {"gather_fragmented": bench_gather(v2, args, stream, "BFloat16")}
+    S, H, D, bs, NB = 64, 8, 128, 16, 65536
+    rng = np.random.default_rng(args.seed + 20)
+    lens = ((rng.integers(512, 8192 + 1, S) + bs - 1) // bs) * bs
+    page = H * bs * D
+    lib = capi.lib()
+    kc, vc = device.DeviceBuffer(NB * page * 2), device.DeviceBuffer(NB * page * 2)
+    device.fill_random(kc.ptr, NB * page, capi.DTYPE_BF16, 1, 5)
+    device.fill_random(vc.ptr, NB * page, capi.DTYPE_BF16, 1, 6)
+    width = int(lens.max()) // bs
+    table = np.full((S, width), 2**64 - 1, np.uint64)
+    nxt = 0
+    for r in range(S):
+        n = int(lens[r]) // bs
+        table[r, :n] = np.arange(nxt, nxt + n, dtype=np.uint64)
+        nxt += n
+    total = int(lens.sum())
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    ko, vo = device.DeviceBuffer(total * H * D * 2), device.DeviceBuffer(total * H * D * 2)
+    td, ld, od = device.to_device(table.reshape(-1)), device.to_device(lens.astype(np.uint64)), device.to_device(offs)
+    device.synchronize()
+
+    def contiguous():
+        capi.check(lib.kvflux_gather_paged_kv(kc.ptr, vc.ptr, NB, H, bs, D, capi.DTYPE_BF16, td.ptr, width, ld.ptr,
+                                              od.ptr, S, int(lens.max()), ko.ptr, vo.ptr, stream))
+
+    ms = time_launches(contiguous, stream, args.warmup, args.steps)
+    moved = 8192 * total + 8 * (total // bs)
+    out["gather_contiguous"] = {"kernel_us": ms * 1e3, "GBps": moved / (ms * 1e-3) / 1e9, "bytes": moved}
+    half = total * H * D * 2  # one output cache: 1.16 GB
+
+    def d2d():
+        capi.call("kvflux_memcpy_async", C.c_void_p(ko.ptr), C.c_void_p(kc.ptr), half, C.c_void_p(stream))
+
+    ms = time_launches(d2d, stream, args.warmup, args.steps)
+    out["memcpy_d2d"] = {"us": ms * 1e3, "GBps": 2 * half / (ms * 1e-3) / 1e9, "bytes": 2 * half}
+
+    def fill():
+        capi.call("kvflux_fill_bytes", C.c_void_p(ko.ptr), 0x3C, half, C.c_void_p(stream))
+        capi.call("kvflux_fill_bytes", C.c_void_p(vo.ptr), 0x3C, half, C.c_void_p(stream))
+
+    ms = time_launches(fill, stream, args.warmup, args.steps)
+    out["write_only"] = {"us": ms * 1e3, "GBps": 2 * half / (ms * 1e-3) / 1e9, "bytes": 2 * half}
+    device.synchronize()
+    t = []
+    for _ in range(args.warmup + args.steps):
+        t0 = time.perf_counter()
+        device.compare_bytes(ko.ptr, vo.ptr, half)
+        t.append(time.perf_counter() - t0)
+    sec = float(np.median(t[args.warmup:]))
+    out["read_only"] = {"us": sec * 1e6, "GBps": 2 * half / sec / 1e9, "bytes": 2 * half,
+                        "note": "synchronous call, host timing (median); rocprof gives the kernel alone"}
+    # The KV write's bytes (4096 tokens x 8 heads x 128 BF16, K and V: 33.6 MB
+    # moved) as a contiguous copy by the same gather kernel, cold: 16 sets of
+    # 256 whole pages and their own outputs, rotated (537 MB in all, past the
+    # 256 MB Infinity Cache) like the cold write.
+    sets, npg = 16, 256
+    outs = [(device.DeviceBuffer(npg * page * 2), device.DeviceBuffer(npg * page * 2)) for _ in range(sets)]
+    tabs = [device.to_device(np.arange(j * npg, (j + 1) * npg, dtype=np.uint64)) for j in range(sets)]
+    one_len, one_off = device.to_device(np.array([npg * bs], np.uint64)), device.to_device(np.zeros(1, np.uint64))
+    device.synchronize()
+    cycle = [0]
+
+    def small_copy():
+        j = cycle[0] % sets
+        cycle[0] += 1
+        capi.check(lib.kvflux_gather_paged_kv(kc.ptr, vc.ptr, NB, H, bs, D, capi.DTYPE_BF16, tabs[j].ptr, npg,
+                                              one_len.ptr, one_off.ptr, 1, npg * bs, outs[j][0].ptr, outs[j][1].ptr,
+                                              stream))
+
+    ms = time_launches(small_copy, stream, sets, sets * max(4, args.steps // 4))
+    moved = 2 * 2 * npg * page * 2
+    out["write_sized_copy_cold"] = {"kernel_us": ms * 1e3, "GBps": moved / (ms * 1e-3) / 1e9, "bytes": moved,
+                                    "sets": sets}
+    for v in out.values():
+        v["pct_of_peak"] = round(100 * v["GBps"] / PEAK_HBM_GBPS, 2)
+    return out
 
 
 def calibrate_copy(args) -> int:
@@ -686,7 +780,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-rows", type=int, default=24, help="decode rows timed on the CPU oracle")
     ap.add_argument("--skip-aux", action="store_true", help="decode only")
-    ap.add_argument("--only", choices=("write", "gather", "prefill", "cow"),
+    ap.add_argument("--only", choices=("write", "gather", "prefill", "cow", "ceilings"),
                     help="run one auxiliary leg alone and print its JSON object (for profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true", help="1 GiB device copy for counter scaling")
     args = ap.parse_args()
@@ -714,7 +808,8 @@ def main() -> int:
         legs = {"write": lambda: bench_write(v2, args, stream.handle),
                 "gather": lambda: bench_gather(v2, args, stream.handle, "BFloat16"),
                 "prefill": lambda: bench_prefill(v2, args, stream.handle),
-                "cow": lambda: bench_cow(v2, args, stream.handle)}
+                "cow": lambda: bench_cow(v2, args, stream.handle),
+                "ceilings": lambda: bench_ceilings(v2, args, stream.handle)}
         log(f"{args.only} ...")
         print(json.dumps({args.only: legs[args.only]()}))
         return 0

@@ -419,11 +419,14 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     // tile's loads (2 * kDma per thread, issued one step earlier), then a
     // barrier publishes the tile; a second barrier frees the buffer.
     const bool tail = ntiles * kPfTile > p.kv_len;  // the last tile has keys past kv_len
-    // Called at the top of a step, before tile `next` is issued: every wave
-    // has issued (read the page list for) all tiles before it, behind the
-    // barrier that ended the previous step.
+    // Called at the top of a step, before tile `next` is issued. The barrier
+    // first: every wave must be past its reads of the page list for the tiles
+    // before `next` (a wave's reads are complete once it has issued that
+    // tile's loads, whose addresses they give). On the first step nothing
+    // else separates the split's first issue() from this restage.
     auto restage = [&](std::uint32_t next) {
         if ((next & win_mask) == 0) {  // uniform
+            lds_barrier();
             stage(first_page(next));
             wait_lgkm0();
             lds_barrier();

@@ -104,45 +104,72 @@ __global__ void fill_random_kernel(void* dst, std::uint64_t count, int dtype, in
     }
 }
 
-__global__ void compare_kernel(const unsigned char* a, const unsigned char* b, std::uint64_t bytes,
-                               unsigned long long* mismatches) {
-    const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+// Streaming form of the two byte kernels (they double as the read-only and
+// write-only bandwidth probes of the benchmark): 512-thread workgroups walk
+// 32 KiB chunks, a thread's four 16-byte accesses per chunk (consecutive
+// lanes on consecutive vectors) all issued before their results are used,
+// with the non-temporal hint (each byte is touched once).
+constexpr int kByteThreads = 512;
+constexpr int kByteVectors = 4;  // 16-byte vectors per thread per chunk
+constexpr std::uint64_t kChunkVectors = kByteThreads * kByteVectors;
+
+__device__ inline unsigned long long differing_bytes(const V16& x, const V16& y) {
+    unsigned long long n = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const std::uint32_t d = x.w[k] ^ y.w[k];
+        n += ((d & 0xffu) != 0) + ((d & 0xff00u) != 0) + ((d & 0xff0000u) != 0) + ((d & 0xff000000u) != 0);
+    }
+    return n;
+}
+
+__global__ __launch_bounds__(kByteThreads) void compare_kernel(const unsigned char* a, const unsigned char* b,
+                                                               std::uint64_t bytes, unsigned long long* mismatches) {
     unsigned long long local = 0;
     const std::uint64_t words = bytes / 16;
+    const std::uint64_t chunks = words / kChunkVectors;
     const auto* a16 = reinterpret_cast<const V16*>(a);
     const auto* b16 = reinterpret_cast<const V16*>(b);
-    for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-         i < words; i += stride) {
-        const V16 x = a16[i], y = b16[i];
+    for (std::uint64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        V16 x[kByteVectors], y[kByteVectors];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const std::uint32_t d = x.w[k] ^ y.w[k];
-            local += ((d & 0xffu) != 0) + ((d & 0xff00u) != 0) + ((d & 0xff0000u) != 0) +
-                     ((d & 0xff000000u) != 0);
+        for (int u = 0; u < kByteVectors; ++u) {
+            const std::uint64_t i = c * kChunkVectors + threadIdx.x + u * kByteThreads;
+            x[u] = stream_load(a16 + i);
+            y[u] = stream_load(b16 + i);
         }
+#pragma unroll
+        for (int u = 0; u < kByteVectors; ++u) local += differing_bytes(x[u], y[u]);
     }
-    for (std::uint64_t i = words * 16 + static_cast<std::uint64_t>(blockIdx.x) * blockDim.x +
-                           threadIdx.x;
-         i < bytes; i += stride) {
-        local += a[i] != b[i];
-    }
+    // Vectors past the last whole chunk, then bytes past the last vector.
+    const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+    const std::uint64_t self = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (std::uint64_t i = chunks * kChunkVectors + self; i < words; i += stride) local += differing_bytes(a16[i], b16[i]);
+    for (std::uint64_t i = words * 16 + self; i < bytes; i += stride) local += a[i] != b[i];
     if (local) atomicAdd(mismatches, local);
 }
 
-__global__ void fill_bytes_kernel(unsigned char* dst, std::uint32_t word, std::uint64_t bytes) {
-    const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+__global__ __launch_bounds__(kByteThreads) void fill_bytes_kernel(unsigned char* dst, std::uint32_t word,
+                                                                  std::uint64_t bytes) {
     const std::uint64_t words = bytes / 16;
+    const std::uint64_t chunks = words / kChunkVectors;
     auto* d16 = reinterpret_cast<V16*>(dst);
     const V16 v{{word, word, word, word}};
-    for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-         i < words; i += stride) {
-        d16[i] = v;
+    for (std::uint64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+#pragma unroll
+        for (int u = 0; u < kByteVectors; ++u) stream_store(d16 + c * kChunkVectors + threadIdx.x + u * kByteThreads, v);
     }
-    for (std::uint64_t i = words * 16 + static_cast<std::uint64_t>(blockIdx.x) * blockDim.x +
-                           threadIdx.x;
-         i < bytes; i += stride) {
-        dst[i] = static_cast<unsigned char>(word);
-    }
+    const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+    const std::uint64_t self = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (std::uint64_t i = chunks * kChunkVectors + self; i < words; i += stride) d16[i] = v;
+    for (std::uint64_t i = words * 16 + self; i < bytes; i += stride) dst[i] = static_cast<unsigned char>(word);
+}
+
+// Workgroups of the byte kernels: one per 32 KiB chunk, at most 4096 (a
+// few resident per CU walk the rest).
+unsigned byte_grid(std::uint64_t bytes) {
+    const std::uint64_t chunks = bytes / (16 * kChunkVectors);
+    return static_cast<unsigned>(chunks < 1 ? 1 : (chunks > 4096 ? 4096 : chunks));
 }
 
 unsigned grid_for(std::uint64_t work, unsigned block) {
@@ -236,7 +263,7 @@ int kvflux_fill_bytes(void* dst, int value, size_t bytes, void* stream) {
     }
     const std::uint32_t b = static_cast<std::uint8_t>(value);
     const std::uint32_t word = b | (b << 8) | (b << 16) | (b << 24);
-    hipLaunchKernelGGL(fill_bytes_kernel, dim3(grid_for(bytes / 16 + 1, 256)), dim3(256), 0,
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3(byte_grid(bytes)), dim3(kByteThreads), 0,
                        as_stream(stream), static_cast<unsigned char*>(dst), word,
                        static_cast<std::uint64_t>(bytes));
     return launch_status("fill_bytes_kernel");
@@ -337,7 +364,7 @@ int kvflux_compare_bytes(const void* a, const void* b, uint64_t bytes, uint64_t*
     status = hip_status(hipMemcpy(counter, &zero, sizeof(zero), hipMemcpyHostToDevice),
                         "reset compare counter");
     if (status == KVFLUX_OK) {
-        hipLaunchKernelGGL(compare_kernel, dim3(grid_for(bytes / 16 + 1, 256)), dim3(256), 0,
+        hipLaunchKernelGGL(compare_kernel, dim3(byte_grid(bytes)), dim3(kByteThreads), 0,
                            nullptr, static_cast<const unsigned char*>(a),
                            static_cast<const unsigned char*>(b), bytes, counter);
         status = launch_status("compare_kernel");

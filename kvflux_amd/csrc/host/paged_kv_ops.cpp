@@ -176,15 +176,19 @@ void read_paged_kv_batch(const PagedKVStorage& storage,
 
 namespace {
 
-bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens,
+// Whether the MFMA prefill takes the call: the precision allows it and the
+// shape is inside the kernel's limits (the same limits kvflux_paged_prefill
+// checks), so its workspace is reserved only for calls that will use it.
+bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len,
                       AttentionPrecision precision) {
     if (precision == AttentionPrecision::Exact) return false;
-    if (layout.dtype() == DType::Float32) return false;
+    if (precision == AttentionPrecision::Auto && query_tokens < 16) return false;
+    if (query_tokens == 0 || layout.dtype() == DType::Float32) return false;
     if (layout.head_size() != 64 && layout.head_size() != 128 && layout.head_size() != 256) return false;
     const std::size_t bs = layout.block_size();
     if (bs > 256 || (bs & (bs - 1)) != 0) return false;  // a power of two up to 256
-    if (precision == AttentionPrecision::Auto && query_tokens < 16) return false;
-    return query_tokens >= 1;
+    return layout.num_blocks() <= 0x7fffffffULL && layout.num_kv_heads() <= 65535 && kv_len <= 0x7fffffffULL &&
+           layout.page_bytes() <= 0xffffffffULL;
 }
 
 } // namespace
@@ -226,7 +230,7 @@ void paged_attention(const PagedKVStorage& storage, const SequenceState& sequenc
     validate_q_o(storage, query_device, output_device, tensor_bytes);
     const auto dev = storage.scratch().upload({{table.data(), table_bytes}});
     bool launched = false;
-    if (prefill_eligible(layout, query_tokens, precision)) {
+    if (prefill_eligible(layout, query_tokens, sequence.num_tokens(), precision)) {
         std::size_t ws_bytes = 0;
         void* ws = prefill_workspace(storage, query_tokens, sequence.num_tokens(), query_heads, &ws_bytes);
         const int status = kvflux_paged_prefill_split(

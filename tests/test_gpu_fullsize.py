@@ -113,6 +113,7 @@ def decode_batch(v2):
     B, H, Hq, D, bs, prefix = 128, 8, 32, 128, 16, 2048
     rng = np.random.default_rng(2024)
     lens = rng.integers(1024, 32768 + 1, B)
+    lens[3] = prefix  # one row that is exactly the shared prefix
     pool = v2.PhysicalBlockPool(1 << 18, bs)
     storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
     fragment(pool, rng.permutation(pool.capacity()))
@@ -147,7 +148,16 @@ def test_decode_full_size_rows_and_repeat(gpu, v2, decode_batch):
     page_elems = H * bs * D
     kb, vb = d["storage"].key_base(), d["storage"].value_base()
     lens = d["lens"]
-    for r in sorted({int(np.argmin(lens)), int(np.argmax(lens)), 5}):
+    # 32+ rows: the shortest, the longest, the prefix-only row, rows just
+    # below and above the prefix length, and a seeded sample of the rest.
+    shared = int(np.flatnonzero(lens == 2048)[0])
+    near = [int(np.argmin(np.where(lens < 2048, 2048 - lens, 1 << 30))),
+            int(np.argmin(np.where(lens > 2048, lens - 2048, 1 << 30)))]
+    picked = {int(np.argmin(lens)), int(np.argmax(lens)), shared, *near}
+    picked |= set(np.random.default_rng(7).choice(d["B"], 40, replace=False).tolist())
+    picked = sorted(picked)[:max(32, len(picked))]
+    assert len(picked) >= 32
+    for r in picked:
         L = int(lens[r])
         ids = v2.build_read_block_table(d["seqs"][r])
         kc = np.concatenate([device.memcpy_d2h(kb + p * page_elems * 2, page_elems * 2, np.uint16) for p in ids])
@@ -171,26 +181,38 @@ def test_decode_full_size_constant_values(gpu, v2, decode_batch):
 
 
 def test_prefill_full_size_sampled_rows(gpu, v2):
-    H, Hq, D, bs, T = 8, 32, 128, 16, 4096
+    """The prefill configuration in full: 8 sequences of 4096 tokens written
+    through slot mappings into random pages of one pool, each prefilled on the
+    MFMA kernel; 16+ rows of every sequence, spread over its length (first and
+    last tokens, tile and page boundaries, a seeded sample), within 2e-2 of
+    the reference attention on that sequence's contiguous K/V."""
+    S, H, Hq, D, bs, T = 8, 8, 32, 128, 16, 4096
     rng = np.random.default_rng(31)
-    pool = v2.PhysicalBlockPool(2 * T // bs + 64, bs)
+    pool = v2.PhysicalBlockPool(S * T // bs + 64, bs)
     storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
     fragment(pool, rng.permutation(pool.capacity()))
-    seq = v2.SequenceState(0, pool)
-    seq.append_tokens(T)
     kn, vn = device.DeviceBuffer(T * H * D * 2), device.DeviceBuffer(T * H * D * 2)
-    device.fill_random(kn.ptr, T * H * D, capi.DTYPE_BF16, 1, 32)
-    device.fill_random(vn.ptr, T * H * D, capi.DTYPE_BF16, 1, 33)
-    v2.write_paged_kv(storage, kn.ptr, vn.ptr, v2.build_slot_mapping([(seq, t) for t in range(T)]))
-    q = oracle.random_elements(0, T * Hq * D, oracle.F32, 1, 34)
-    qd, od = buffer_like(q), buffer_like(np.zeros(q.size, np.float32))
-    v2.paged_attention(storage, seq, qd.ptr, od.ptr, T, Hq, v2.AttentionPrecision.Fast)
-    got = od.download(np.float32).reshape(T, Hq * D)
-    k_host = kn.download(np.uint16).reshape(T, H, D)
-    v_host = vn.download(np.uint16).reshape(T, H, D)
-    qr = q.reshape(T, Hq * D)
-    for t in sorted({0, 1, 15, 16, 1000, 2047, 2048, 4094, 4095} | set(rng.integers(0, T, 6).tolist())):
-        # token t sees tokens 0..t: contiguous K/V of those tokens, one query row
-        exp = oracle.reference_attention(qr[t], oracle.decode(k_host[:t + 1].reshape(-1), oracle.BF16),
-                                         oracle.decode(v_host[:t + 1].reshape(-1), oracle.BF16), 1, t + 1, Hq, H, D)
-        assert np.abs(got[t] - exp).max() < 2e-2, t
+    qd, od = device.DeviceBuffer(T * Hq * D * 4), device.DeviceBuffer(T * Hq * D * 4)
+    seqs = []  # all eight stay alive: their pages are distinct
+    for i in range(S):
+        seq = v2.SequenceState(i, pool)
+        seqs.append(seq)
+        seq.append_tokens(T)
+        device.fill_random(kn.ptr, T * H * D, capi.DTYPE_BF16, 1, 32 + 3 * i)
+        device.fill_random(vn.ptr, T * H * D, capi.DTYPE_BF16, 1, 33 + 3 * i)
+        v2.write_paged_kv(storage, kn.ptr, vn.ptr, v2.build_slot_mapping([(seq, t) for t in range(T)]))
+        q = oracle.random_elements(0, T * Hq * D, oracle.F32, 1, 34 + 3 * i)
+        qd.upload(q)
+        v2.paged_attention(storage, seq, qd.ptr, od.ptr, T, Hq, v2.AttentionPrecision.Fast)
+        got = od.download(np.float32).reshape(T, Hq * D)
+        assert np.all(np.isfinite(got))
+        k_host = kn.download(np.uint16).reshape(T, H, D)
+        v_host = vn.download(np.uint16).reshape(T, H, D)
+        qr = q.reshape(T, Hq * D)
+        rows = {0, 1, 15, 16, 63, 64, 1000, 2047, 2048, 4094, 4095} | set(rng.integers(0, T, 6).tolist())
+        for t in sorted(rows):
+            # token t sees tokens 0..t: contiguous K/V of those tokens, one query row
+            exp = oracle.reference_attention(qr[t], oracle.decode(k_host[:t + 1].reshape(-1), oracle.BF16),
+                                             oracle.decode(v_host[:t + 1].reshape(-1), oracle.BF16), 1, t + 1,
+                                             Hq, H, D)
+            assert np.abs(got[t] - exp).max() < 2e-2, (i, t)

@@ -246,6 +246,11 @@ SPLIT_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("BFloat16", 2, 8, 128, 16, 3000, 1),      # one query token (Fast precision sends it here)
     ("Float16", 1, 6, 64, 64, 2500, 2),        # group 6 with two tokens
     ("BFloat16", 2, 8, 128, 128, 6000, 64),    # 128-token pages
+    # A split starting one tile before a page-list window boundary (2048
+    # pages = 32 tiles at block_size 1, 512 tiles at 16): the window is
+    # restaged right after the split's first tile is issued.
+    ("BFloat16", 1, 4, 128, 1, 63300, 16),     # 31 tiles per split: split 1 starts at tile 31
+    ("BFloat16", 1, 4, 128, 16, 148000, 16),   # 73 tiles per split: split 7 starts at tile 511
 ]
 
 

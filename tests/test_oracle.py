@@ -214,3 +214,66 @@ def test_counter_generator_properties():
     assert np.array_equal(part, n[1234:1244])
     b = oracle.random_elements(0, 1000, oracle.BF16, 1, 6)
     assert np.array_equal(b, np.array([exact_bf16(x) for x in n[:1000]], np.uint16))
+
+
+def _fragmented_case(dtype, kv_heads, block_size, head_size, pages, seed):
+    """A cache of `pages` pages filled with random elements of `dtype`
+    (NaN-free), and a seeded permutation to draw non-contiguous tables from."""
+    rng = np.random.default_rng(seed)
+    n = pages * kv_heads * block_size * head_size
+    k = oracle.random_elements(0, n, dtype, 0, seed * 10 + 1)
+    v = oracle.random_elements(0, n, dtype, 0, seed * 10 + 2)
+    return k, v, rng.permutation(pages).astype(np.uint64), rng
+
+
+PAGED_CASES = [  # dtype, kv_heads, q_heads, block_size, head_size
+    (oracle.F32, 2, 4, 16, 64),
+    (oracle.BF16, 2, 8, 3, 32),
+    (oracle.F16, 1, 3, 1, 5),
+    (oracle.BF16, 4, 4, 7, 16),
+]
+
+
+@pytest.mark.parametrize("dtype,kv_heads,q_heads,block_size,head_size", PAGED_CASES)
+def test_paged_oracle_is_gather_then_reference_attention(dtype, kv_heads, q_heads, block_size, head_size):
+    """The paged oracle functions the GPU parity tests check against,
+    oracle_paged_attention_rows and oracle_paged_attention_causal, against
+    the two-path composition of the reference's own attention test
+    (tests/paged_attention_test.cu:86-110): gather each sequence's pages to
+    contiguous K/V, then the pinned reference_attention. Fragmented random
+    tables, tail pages of every fill, lengths 1 and a page multiple;
+    bit-exact, on one thread and on four."""
+    pages = 96
+    k, v, order, rng = _fragmented_case(dtype, kv_heads, block_size, head_size, pages, head_size + block_size)
+    width = pages // 4
+    lens = np.array([1, block_size, block_size * 3 + 1, width * block_size, 37, 2 * block_size - 1], np.uint64)
+    lens = np.minimum(lens, width * block_size)
+    tables = np.stack([order[(7 * r) % (pages - width):][:width] for r in range(len(lens))])
+    rows = len(lens)
+    q = oracle.random_elements(0, rows * q_heads * head_size, oracle.F32, 0, 99 + head_size)
+    expected = np.empty(rows * q_heads * head_size, np.float32)
+    for r in range(rows):
+        L = int(lens[r])
+        kg, vg = oracle.gather_paged_kv(k, v, kv_heads, block_size, head_size, dtype, tables[r], L)
+        qr = q[r * q_heads * head_size:(r + 1) * q_heads * head_size]
+        expected[r * q_heads * head_size:(r + 1) * q_heads * head_size] = oracle.reference_attention(
+            qr, oracle.decode(kg, dtype), oracle.decode(vg, dtype), 1, L, q_heads, kv_heads, head_size)
+    for threads in (1, 4):
+        got = oracle.paged_attention_rows(k, v, kv_heads, block_size, head_size, dtype, tables.reshape(-1), width,
+                                          lens, q, q_heads, threads=threads)
+        assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+    # causal trailing queries of one sequence
+    kv_len = int(width * block_size - block_size // 2)
+    tq = min(9, kv_len)
+    qc = oracle.random_elements(0, tq * q_heads * head_size, oracle.F32, 0, 7 + head_size)
+    kg, vg = oracle.gather_paged_kv(k, v, kv_heads, block_size, head_size, dtype, tables[2], kv_len)
+    exp_c = oracle.reference_attention(qc, oracle.decode(kg, dtype), oracle.decode(vg, dtype), tq, kv_len, q_heads,
+                                       kv_heads, head_size)
+    for threads in (1, 4):
+        got_c = oracle.paged_attention_causal(k, v, kv_heads, block_size, head_size, dtype, tables[2], kv_len, qc, tq,
+                                              q_heads, threads=threads)
+        assert np.array_equal(got_c.view(np.uint32), exp_c.view(np.uint32))
+    # a plausible indexing mistake (a row reading its neighbour's table) is caught
+    wrong = oracle.paged_attention_rows(k, v, kv_heads, block_size, head_size, dtype, tables[::-1].reshape(-1), width,
+                                        lens, q, q_heads)
+    assert not np.array_equal(wrong.view(np.uint32), expected.view(np.uint32))
