@@ -104,10 +104,10 @@ def bench_decode(v2, args, stream):
     from kvflux_amd import capi, device
     from oracle import oracle
 
-    B, H, Hq, D, bs, prefix = 128, 8, 32, 128, 16, 2048
+    B, H, Hq, D, bs, prefix = 128, 8, 32, 128, args.block_size, 2048
     rng = np.random.default_rng(args.seed)
     lens = rng.integers(1024, 32768 + 1, B)
-    pool = v2.PhysicalBlockPool(1 << 18, bs)
+    pool = v2.PhysicalBlockPool((1 << 22) // bs, bs)  # 2^22 tokens of room
     storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
     fragment_pool(pool, rng.permutation(pool.capacity()))
     cache = v2.PrefixCache(pool)
@@ -780,6 +780,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-rows", type=int, default=24, help="decode rows timed on the CPU oracle")
     ap.add_argument("--skip-aux", action="store_true", help="decode only")
+    ap.add_argument("--block-size", type=int, default=16, help="page size of the decode batch (16 is the benchmark)")
     ap.add_argument("--only", choices=("write", "gather", "prefill", "cow", "ceilings"),
                     help="run one auxiliary leg alone and print its JSON object (for profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true", help="1 GiB device copy for counter scaling")

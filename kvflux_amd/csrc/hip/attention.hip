@@ -184,6 +184,11 @@ struct Params {
     // Block-size-16 kernel: log2(block_size / 16) (pages of 16 to 128
     // tokens are cut into 16-token tiles).
     std::uint32_t page_tiles_shift;
+    // Block-size-16 kernel on pages of 1 to 8 tokens: log2(16 / block_size)
+    // (a 16-token tile gathers its rows from that many pages) and
+    // log2(block_size); both 0 for pages of 16 tokens or more.
+    std::uint32_t tile_pages_shift;
+    std::uint32_t bs_shift;
 };
 
 __device__ inline std::uint64_t row_length(const Params& p, std::uint32_t row) {
@@ -583,7 +588,13 @@ __device__ inline std::uint32_t route(std::uint32_t hi, std::uint32_t mid, std::
 
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
-template <typename E, int kD, int kG>
+// kSmall: pages of 1 to 8 tokens. A 16-token tile then spans
+// 2^tile_pages_shift pages; lane j of a wave holds the offset of page slot j
+// of the wave's tiles (tile j >> tile_pages_shift, page j & mask of it; the
+// item size keeps them within 64), and every lane takes the page of its own
+// token row from the lane holding it (a cross-lane read), where whole tiles
+// take one wave-uniform page.
+template <typename E, int kD, int kG, bool kSmall>
 __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p) {
     using M = Mfma<E>;
     using Vec = typename M::Vec;
@@ -599,8 +610,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     constexpr int kRowBytes = kD * 2;
     constexpr int kQPer = (kG * kD + kThreads - 1) / kThreads;
     static_assert(kRowStep * kVLoads == kBs, "V tile covers 16 tokens");
-    // Chunk of 2^chunk_shift tokens (512..4096): 32..256 tiles per item, so
-    // 8..64 (even) tiles per wavefront, whose page offsets fit one lane each.
+    // Chunk of 2^chunk_shift tokens (256..4096): 16..256 tiles per item, so
+    // 4..64 (even) tiles per wavefront, whose page offsets fit one lane each
+    // (small pages: whose page slots fit one lane each).
     const std::uint32_t chunk_shift = p.chunk_shift;
     const std::uint32_t chunk_tokens = 1u << chunk_shift;
     const std::uint32_t tiles = chunk_tokens / kBs;  // tiles per item
@@ -661,9 +673,14 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     const T* kc = static_cast<const T*>(p.key_cache);
     const T* vc = static_cast<const T*>(p.value_cache);
     // A page holds 2^page_tiles_shift 16-token tiles of every kv head:
-    // tile t of a row is tile t % 2^shift of page t >> shift.
+    // tile t of a row is tile t % 2^shift of page t >> shift. Small pages
+    // (kSmall): 2^tile_pages_shift pages per tile, one kv head's block of a
+    // page being bs rows.
     const std::uint32_t tile_shift = p.page_tiles_shift;
-    const std::uint64_t head_stride = static_cast<std::uint64_t>(kBs << tile_shift) * kD;
+    const std::uint32_t tps = kSmall ? p.tile_pages_shift : 0u;
+    const std::uint32_t bs_shift = p.bs_shift;
+    const std::uint64_t head_stride =
+        kSmall ? (static_cast<std::uint64_t>(1) << bs_shift) * kD : static_cast<std::uint64_t>(kBs << tile_shift) * kD;
     const std::uint64_t page_stride = head_stride * p.heads;
     // K: lane (quad, col) loads token col, dims 8*quad + 32*kk .. +8.
     const std::uint32_t k_lane = col * kD + quad * 8;
@@ -711,14 +728,31 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         return it;
     };
     // Lane j < per_wave of every wave: element offset of the page of tile
-    // wave + kWaves * j, or kNoPage.
+    // wave + kWaves * j, or kNoPage. Small pages: lane j < per_wave << tps
+    // holds page slot j (page j & (2^tps - 1) of tile wave + kWaves * (j >> tps)).
     auto fetch_pages = [&](const Item& it) -> std::uint64_t {
         const std::uint64_t* table_row = p.table + (p.seq_lens ? it.row : 0) * p.width;
-        const std::uint64_t tile = static_cast<std::uint64_t>(it.chunk) * tiles + wave + kWaves * (lane & (per_wave - 1));
-        const std::uint64_t logical = tile >> tile_shift;
-        const std::uint64_t id = table_row[logical < p.width ? logical : p.width - 1];
-        const std::uint64_t in_page = (tile & ((1u << tile_shift) - 1)) * (kBs * kD);
-        return logical < p.width && id < p.num_blocks ? id * page_stride + in_page : kNoPage;
+        if constexpr (kSmall) {
+            const std::uint32_t j = lane & ((per_wave << tps) - 1);
+            const std::uint64_t tile = static_cast<std::uint64_t>(it.chunk) * tiles + wave + kWaves * (j >> tps);
+            const std::uint64_t logical = (tile << tps) + (j & ((1u << tps) - 1));
+            const std::uint64_t id = table_row[logical < p.width ? logical : p.width - 1];
+            return logical < p.width && id < p.num_blocks ? id * page_stride : kNoPage;
+        } else {
+            const std::uint64_t tile = static_cast<std::uint64_t>(it.chunk) * tiles + wave + kWaves * (lane & (per_wave - 1));
+            const std::uint64_t logical = tile >> tile_shift;
+            const std::uint64_t id = table_row[logical < p.width ? logical : p.width - 1];
+            const std::uint64_t in_page = (tile & ((1u << tile_shift) - 1)) * (kBs * kD);
+            return logical < p.width && id < p.num_blocks ? id * page_stride + in_page : kNoPage;
+        }
+    };
+    // Small pages: the offset page slot `slot` holds, read from its lane
+    // (kNoPage reads page 0; such rows are masked).
+    auto slot_offset = [](std::uint64_t pages, std::uint32_t slot) -> std::uint64_t {
+        const auto lo32 = static_cast<std::uint32_t>(__shfl(static_cast<int>(pages), static_cast<int>(slot)));
+        const auto hi32 = static_cast<std::uint32_t>(__shfl(static_cast<int>(pages >> 32), static_cast<int>(slot)));
+        const std::uint64_t off = (static_cast<std::uint64_t>(hi32) << 32) | lo32;
+        return off == kNoPage ? 0 : off;
     };
     // Query elements tid + kThreads * i of the item's kG heads (clamped).
     auto fetch_query = [&](const Item& it, float (&q)[kQPer]) {
@@ -765,6 +799,32 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         // K loads take 64 bytes of each of 16 token rows, so a 128-byte line
         // is completed by a second load and K keeps the default policy.
         for (int i = 0; i < kVLoads; ++i) b.v[i] = stream_load(reinterpret_cast<const uint4*>(vb + i * 512));
+    };
+    // Small pages: tile `jt` of the wave in `pages` (slots jt << tps ..).
+    // Token t of the tile is row t & (bs - 1) of slot (jt << tps) + (t >> bs_shift).
+    auto load_small = [&](std::uint64_t pages, std::uint32_t jt, std::uint32_t kvh, Tile& b) {
+        const std::uint32_t first = jt << tps;
+        const std::uint32_t bs_mask = (1u << bs_shift) - 1;
+        const std::uint64_t head = kvh * head_stride;
+        {
+            const std::uint32_t t = static_cast<std::uint32_t>(col);
+            const T* kb = kc + slot_offset(pages, first + (t >> bs_shift)) + head + (t & bs_mask) * kD + quad * 8;
+#pragma unroll
+            for (int kk = 0; kk < kSteps; ++kk) b.k[kk] = *reinterpret_cast<const uint4*>(kb + kk * 32);
+        }
+#pragma unroll
+        for (int i = 0; i < kVLoads; ++i) {
+            const std::uint32_t t = static_cast<std::uint32_t>(lane / kCpr + i * kRowStep);
+            const T* vb = vc + slot_offset(pages, first + (t >> bs_shift)) + head + (t & bs_mask) * kD + (lane % kCpr) * 8;
+            b.v[i] = stream_load(reinterpret_cast<const uint4*>(vb));
+        }
+    };
+    // Leading valid pages of tile jt (small pages): those before the tile's
+    // first missing page slot, from a wave-wide ballot of missing slots.
+    auto leading_pages = [&](std::uint64_t missing, std::uint32_t jt) -> std::uint32_t {
+        const std::uint32_t n = 1u << tps;
+        const std::uint64_t bits = (missing >> (jt << tps)) & ((n == 64 ? ~0ULL : (1ULL << n) - 1));
+        return bits ? static_cast<std::uint32_t>(__builtin_ctzll(bits)) : n;
     };
 
     // run_max is a reference point, not always the exact maximum: it only
@@ -886,8 +946,13 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     }
     __syncthreads();
     Tile buf0, buf1;
-    load(page_of(cur_pages, 0), cur.kvh, buf0);
-    load(page_of(cur_pages, 1), cur.kvh, buf1);
+    if constexpr (kSmall) {
+        load_small(cur_pages, 0, cur.kvh, buf0);
+        load_small(cur_pages, 1, cur.kvh, buf1);
+    } else {
+        load(page_of(cur_pages, 0), cur.kvh, buf0);
+        load(page_of(cur_pages, 1), cur.kvh, buf1);
+    }
     while (true) {
         const std::uint32_t next_item = item + gridDim.x;
         const bool has_next = next_item < total;
@@ -916,14 +981,26 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) acc[m][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+        const std::uint64_t cur_missing = kSmall ? __builtin_amdgcn_ballot_w64(cur_pages == kNoPage) : 0;
         auto valid_of = [&](int j) -> std::uint32_t {
             const std::uint32_t t = wave + kWaves * j;
             const std::uint32_t begin = t * kBs;
             const std::uint32_t n = cur.ntok > begin ? (cur.ntok - begin < kBs ? cur.ntok - begin : kBs) : 0u;
-            return page_of(cur_pages, j) == kNoPage ? 0u : n;
+            if constexpr (kSmall) {
+                const std::uint32_t ok = leading_pages(cur_missing, static_cast<std::uint32_t>(j)) << bs_shift;
+                return n < ok ? n : ok;
+            } else {
+                return page_of(cur_pages, j) == kNoPage ? 0u : n;
+            }
         };
         auto issue = [&](int j, Tile& b) {  // stream position j: this item's tile j or the next item's j - per_wave
-            if (j < per_wave) {
+            if constexpr (kSmall) {
+                if (j < per_wave) {
+                    load_small(cur_pages, static_cast<std::uint32_t>(j), cur.kvh, b);
+                } else {
+                    load_small(nxt_pages, static_cast<std::uint32_t>(j - per_wave), nxt.kvh, b);
+                }
+            } else if (j < per_wave) {
                 load(page_of(cur_pages, j), cur.kvh, b);
             } else {
                 load(page_of(nxt_pages, j - per_wave), nxt.kvh, b);
@@ -1163,7 +1240,7 @@ __global__ __launch_bounds__(64) void paged_attention_generic_kernel(Params p, s
 // once per (kernel, device). Devices past kMaxDevices are queried per call.
 constexpr int kMaxDevices = 64;
 
-template <typename E, int kD, int kG>
+template <typename E, int kD, int kG, bool kSmall>
 int resident_slots(int* out) {
     static std::atomic<int> cache[kMaxDevices];
     int device = 0;
@@ -1181,7 +1258,7 @@ int resident_slots(int* out) {
                         "hipDeviceGetAttribute");
     if (status == KVFLUX_OK)
         status = hip_status(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                &per_cu, paged_decode_bs16_kernel<E, kD, kG>, kThreads, 0),
+                                &per_cu, paged_decode_bs16_kernel<E, kD, kG, kSmall>, kThreads, 0),
                             "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (status != KVFLUX_OK) return status;
     const int slots = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
@@ -1195,23 +1272,59 @@ enum class Family { Bs16, Split, Generic };
 struct Plan {
     Family family = Family::Generic;
     std::uint32_t sub = 0;     // Bs16: query heads per launch (divides the group, <= 8)
+    bool small = false;        // Bs16: pages of 1 to 8 tokens
     std::uint32_t shift = 9;   // Bs16: log2(tokens per work item)
     unsigned grid = 0;         // Bs16: persistent grid
     std::uint64_t chunks = 0;  // partial slots per (row, query head); <= 1: no partials
 };
 
-template <typename E, int kD>
+template <typename E, int kD, bool kSmall>
 int resident_slots_for(std::uint32_t sub, int* out) {
     switch (sub) {
-    case 1: return resident_slots<E, kD, 1>(out);
-    case 2: return resident_slots<E, kD, 2>(out);
-    case 3: return resident_slots<E, kD, 3>(out);
-    case 4: return resident_slots<E, kD, 4>(out);
-    case 5: return resident_slots<E, kD, 5>(out);
-    case 6: return resident_slots<E, kD, 6>(out);
-    case 7: return resident_slots<E, kD, 7>(out);
-    default: return resident_slots<E, kD, 8>(out);
+    case 1: return resident_slots<E, kD, 1, kSmall>(out);
+    case 2: return resident_slots<E, kD, 2, kSmall>(out);
+    case 3: return resident_slots<E, kD, 3, kSmall>(out);
+    case 4: return resident_slots<E, kD, 4, kSmall>(out);
+    case 5: return resident_slots<E, kD, 5, kSmall>(out);
+    default: break;
     }
+    if constexpr (kSmall && kD == 128) {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %u", sub);
+    } else {
+        switch (sub) {
+        case 6: return resident_slots<E, kD, 6, kSmall>(out);
+        case 7: return resident_slots<E, kD, 7, kSmall>(out);
+        default: return resident_slots<E, kD, 8, kSmall>(out);
+        }
+    }
+}
+
+// log2 of a power of two.
+inline std::uint32_t log2_pow2(std::uint64_t x) {
+    std::uint32_t l = 0;
+    while ((std::uint64_t{1} << l) < x) ++l;
+    return l;
+}
+
+// Work-item tokens of the block-size-16 kernel: 2^shift with shift in
+// [9, 12] (32..256 tiles per item); pages of bs < 16 tokens cap it at
+// 4096 * bs / 16 (the item's page slots fit one per lane of a wave), down to
+// 256 tokens at bs = 1.
+inline std::uint32_t min_item_shift(std::uint32_t bs) { return bs >= 2 ? 9u : 8u; }
+inline std::uint32_t max_item_shift(std::uint32_t bs) { return bs >= 16 ? 12u : 8u + log2_pow2(bs); }
+
+constexpr std::uint32_t kSmallMaxGroup128 = 5;
+
+// The VALU kernels: split (groups 1, 2, 4, 8) or generic.
+inline int plan_fallback(std::uint64_t group, std::uint64_t max_chunks, Plan* plan) {
+    if (group == 1 || group == 2 || group == 4 || group == 8) {
+        plan->family = Family::Split;
+        plan->chunks = max_chunks;
+    } else {
+        plan->family = Family::Generic;
+        plan->chunks = 0;
+    }
+    return KVFLUX_OK;
 }
 
 // max_chunks: ceil(kv_len / kChunk), the partial count at 512-token items.
@@ -1222,8 +1335,10 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
         // The kernel counts work items in 32 bits (at most 512-token chunks);
         // rows <= kPlanRows keeps the product below 2^51.
         const std::uint32_t bs = p.block_size.divisor;
-        if ((bs == 16 || bs == 32 || bs == 64 || bs == 128) && rows <= kPlanRows && p.width > 0 &&
-            rows * max_chunks * p.heads <= 0xffffffffULL) {
+        const bool small = bs == 1 || bs == 2 || bs == 4 || bs == 8;
+        // Items are counted in 32 bits; at most 2 * max_chunks of them.
+        if ((small || bs == 16 || bs == 32 || bs == 64 || bs == 128) && rows <= kPlanRows && p.width > 0 &&
+            2 * rows * max_chunks * p.heads <= 0xffffffffULL) {
             // A group above 8 runs as launches of a sub-group: the largest
             // divisor of the group up to 8, each launch serving its slice of
             // the query heads (and reading K/V again); the chunk partials of
@@ -1234,14 +1349,18 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             const auto g = static_cast<std::uint32_t>(group);
             std::uint32_t sub = g < 8 ? g : 8;
             while (g % sub != 0) --sub;
+            // Small pages at head_size 128 take groups up to 5 (the per-lane
+            // page addresses of larger groups exceed the registers).
+            if (small && kD == 128 && sub > kSmallMaxGroup128) return plan_fallback(group, max_chunks, plan);
             int slots = 0;
-            const int status = resident_slots_for<E, kD>(sub, &slots);
+            const int status = small ? resident_slots_for<E, kD, true>(sub, &slots)
+                                     : resident_slots_for<E, kD, false>(sub, &slots);
             if (status != KVFLUX_OK) return status;
-            // Work item size: the largest chunk (512, 1024, 2048 or 4096
-            // tokens) that still gives at least 8 items per resident
+            // Work item size: the largest chunk (up to 4096 tokens, less for
+            // small pages) that still gives at least 8 items per resident
             // workgroup when every row is kv_len long.
-            std::uint32_t shift = 9;
-            while (shift < 12) {
+            std::uint32_t shift = min_item_shift(bs);
+            while (shift < max_item_shift(bs)) {
                 const std::uint64_t wider =
                     ((p.kv_len + (std::uint64_t{2} << shift) - 1) >> (shift + 1)) * rows * p.heads;
                 if (wider < 8 * static_cast<std::uint64_t>(slots)) break;
@@ -1251,20 +1370,14 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             const std::uint64_t items = rows * chunks * p.heads;  // upper bound of the real count
             plan->family = Family::Bs16;
             plan->sub = sub;
+            plan->small = small;
             plan->shift = shift;
             plan->grid = static_cast<unsigned>(items == 0 ? 1 : items < static_cast<std::uint64_t>(slots) ? items : slots);
             plan->chunks = chunks;
             return KVFLUX_OK;
         }
     }
-    if (group == 1 || group == 2 || group == 4 || group == 8) {
-        plan->family = Family::Split;
-        plan->chunks = max_chunks;
-    } else {
-        plan->family = Family::Generic;
-        plan->chunks = 0;
-    }
-    return KVFLUX_OK;
+    return plan_fallback(group, max_chunks, plan);
 }
 
 template <typename E>
@@ -1336,14 +1449,24 @@ int launch_generic(Params p, std::uint64_t rows, std::uint64_t head_dim, hipStre
 template <typename E, int kD, int kG>
 int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
     p.row_base = 0;
-    hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG>), dim3(plan.grid), dim3(kThreads), 0, s, p);
+    if (plan.small) {
+        if constexpr (kD != 128 || kG <= static_cast<int>(kSmallMaxGroup128)) {
+            hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, true>), dim3(plan.grid), dim3(kThreads), 0, s, p);
+        } else {
+            return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %d", kG);
+        }
+    } else {
+        hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, false>), dim3(plan.grid), dim3(kThreads), 0, s, p);
+    }
     return launch_status("paged_decode_bs16_kernel");
 }
 
 template <typename E, int kD>
 int run_bs16(Params p, const Plan& plan, hipStream_t s) {
     const std::uint32_t bs = p.block_size.divisor;
-    p.page_tiles_shift = bs == 16 ? 0u : bs == 32 ? 1u : bs == 64 ? 2u : 3u;
+    p.page_tiles_shift = bs <= 16 ? 0u : bs == 32 ? 1u : bs == 64 ? 2u : 3u;
+    p.tile_pages_shift = bs < 16 ? 4u - log2_pow2(bs) : 0u;
+    p.bs_shift = log2_pow2(bs);
     p.chunk_shift = plan.shift;
     const std::uint32_t g = p.q_group;
     for (std::uint32_t first = 0; first < g; first += plan.sub) {
@@ -1495,14 +1618,16 @@ extern "C" int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t
                                                      uint64_t num_kv_heads, uint64_t query_heads,
                                                      uint64_t block_size, uint64_t head_size,
                                                      size_t* bytes) {
-    (void)block_size;
     if (!bytes) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "bytes is null");
     *bytes = 0;
     if (num_kv_heads == 0 || query_heads == 0 || query_heads % num_kv_heads != 0) {
         return fail(KVFLUX_ERR_INVALID_ARGUMENT, "invalid attention head counts");
     }
     if (!uses_split(head_size, query_heads / num_kv_heads)) return KVFLUX_OK;
-    const std::uint64_t chunks = (kv_len + kChunk - 1) / kChunk;
+    // Partials of the smallest work item any kernel uses for this call:
+    // 512 tokens, 256 on pages of one token.
+    const std::uint64_t item = block_size == 1 ? std::uint64_t{1} << min_item_shift(1) : kChunk;
+    const std::uint64_t chunks = (kv_len + item - 1) / item;
     if (chunks <= 1) return KVFLUX_OK;
     const long double need = static_cast<long double>(num_rows) * query_heads * chunks *
                              (head_size + 2) * sizeof(float);

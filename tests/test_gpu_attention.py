@@ -338,6 +338,12 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
     ("BFloat16", 128, 128, 1, 8),
     ("BFloat16", 64, 128, 2, 6),
     ("BFloat16", 8, 128, 2, 8),
+    ("BFloat16", 1, 128, 2, 8),
+    ("Float16", 2, 64, 2, 16),
+    ("BFloat16", 4, 128, 1, 5),
+    ("Float16", 8, 64, 1, 8),
+    ("BFloat16", 8, 128, 1, 6),   # group 6 at head_size 128: small pages stay on the split kernel
+    ("BFloat16", 4, 64, 4, 28),   # group 7 at head_size 64 on the small-page kernel
 ]
 
 
@@ -345,9 +351,11 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
 def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     """Pages of 32, 64 and 128 tokens run on the block-size-16 kernel as
     16-token tiles (a contiguous part of one kv head's rows of a page);
-    block size 8 stays on the split kernel. Lengths sit on tile and page
-    boundaries; table entries past a row's pages are poisoned. Matches the
-    oracle at 1e-5, bit-identical on repeat."""
+    pages of 1, 2, 4 and 8 tokens too, each 16-token tile gathering its rows
+    from 16 / block_size pages (groups above 5 at head_size 128 stay on the
+    split kernel). Lengths sit on tile and page boundaries; table entries
+    past a row's pages are poisoned, so a tile's last pages can be missing.
+    Matches the oracle at 1e-5, bit-identical on repeat."""
     lib = capi.lib()
     P = 512
     code = DTYPES[name][0]
@@ -357,7 +365,7 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     device.fill_random(kc.ptr, P * page, code, 1, 41)
     device.fill_random(vc.ptr, P * page, code, 1, 42)
     rng = np.random.default_rng(bs * 7 + Hq)
-    lens = np.array([1, 15, 16, 17, bs - 1, bs, bs + 1, 2 * bs + 16, 511, 512, 513, 3000, 4096, 4111],
+    lens = np.array([1, 15, 16, 17, max(1, bs - 1), bs, bs + 1, 2 * bs + 16, 511, 512, 513, 3000, 4096, 4111],
                     np.uint64)
     rows = lens.size
     max_len = int(lens.max())
@@ -383,3 +391,43 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table.reshape(-1), width, lens, q, Hq,
                                       threads=8)
     assert np.abs(outs[0] - exp).max() < TOL
+
+
+@pytest.mark.parametrize("name,bs,head_size", [("BFloat16", 8, 128), ("BFloat16", 1, 128), ("Float16", 4, 64)])
+def test_decode_small_pages_item_sizes(gpu, name, bs, head_size):
+    """Small pages cap the work item at 256 * block_size tokens (the item's
+    page slots fit one lane each): 128 rows of up to 20000 tokens with 4 kv
+    heads take items of 2048 tokens at block_size 8, 1024 at 4 and 256 at 1.
+    Sampled rows, including item boundaries, match the oracle at 1e-5."""
+    lib = capi.lib()
+    H, Hq, rows, max_len, P = 4, 16, 128, 20000, 8192
+    code = DTYPES[name][0]
+    page = H * bs * head_size
+    kc, vc = device.DeviceBuffer(P * page * 2), device.DeviceBuffer(P * page * 2)
+    device.fill_random(kc.ptr, P * page, code, 1, 51)
+    device.fill_random(vc.ptr, P * page, code, 1, 52)
+    rng = np.random.default_rng(bs * 131 + head_size)
+    item = 256 * bs
+    edges = [1, item - 1, item, item + 1, 2 * item + bs // 2 + 1, max_len - 1, max_len]
+    lens = np.concatenate([np.array(edges), rng.integers(1, max_len + 1, rows - len(edges))]).astype(np.uint64)
+    width = (max_len + bs - 1) // bs
+    table = rng.integers(0, P, (rows, width)).astype(np.uint64)
+    for r in range(rows):
+        table[r, (int(lens[r]) + bs - 1) // bs:] = 2**64 - 1
+    td, ld = buffer_like(table.reshape(-1)), buffer_like(lens)
+    q = oracle.random_elements(0, rows * Hq * head_size, oracle.F32, 1, 53)
+    qd = buffer_like(q)
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_attention_workspace_size(rows, max_len, H, Hq, bs, head_size, C.byref(ws)))
+    wd = device.DeviceBuffer(max(ws.value, 256))
+    od = buffer_like(np.full(q.size, 7.0, np.float32))
+    capi.check(lib.kvflux_paged_attention(kc.ptr, vc.ptr, P, H, bs, head_size, code, td.ptr, width, ld.ptr,
+                                          max_len, rows, Hq, qd.ptr, od.ptr, wd.ptr, ws.value, None))
+    device.synchronize()
+    got = od.download(np.float32).reshape(rows, -1)
+    assert np.all(np.isfinite(got))
+    sample = np.array(sorted(set(range(len(edges))) | set(rng.choice(rows, 5, replace=False).tolist())))
+    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table[sample].reshape(-1), width,
+                                      lens[sample], q.reshape(rows, -1)[sample].reshape(-1), Hq, threads=8)
+    assert np.abs(got[sample].reshape(-1) - exp).max() < TOL
