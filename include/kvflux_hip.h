@@ -219,6 +219,28 @@ int kvflux_paged_prefill_split(const void* key_cache, const void* value_cache,
                                uint64_t query_heads, const float* query, float* output,
                                void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* kvflux_paged_prefill_batch: kvflux_paged_prefill over num_seqs sequences in
+ * one launch (a prefill batch). Sequence i: table row i of block_table
+ * (device uint64 [num_seqs][max_blocks_per_seq], the reference's
+ * BatchBlockTable layout), kv_lens[i] tokens of which the last
+ * query_lens[i] are its queries, at token rows query_offsets[i] .. of query
+ * and output ([total query tokens][query_heads][head_size] FP32); kv_lens,
+ * query_lens, query_offsets are device uint64 [num_seqs]. max_query_tokens
+ * and max_kv_len (host values) bound every query_lens[i] and kv_lens[i] and
+ * size the grid; max_blocks_per_seq * block_size >= max_kv_len. Workgroups
+ * take the heaviest query blocks of every sequence first. Same arithmetic,
+ * errors and limits as kvflux_paged_prefill (each sequence's outputs are
+ * bit-identical to that call's). Replaces one paged_attention call per
+ * prompt (reference src/v2/paged_attention.cu:193-246) for a batch of
+ * prompts. */
+int kvflux_paged_prefill_batch(const void* key_cache, const void* value_cache, uint64_t num_blocks,
+                               uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size, int dtype,
+                               const uint64_t* block_table, uint64_t max_blocks_per_seq,
+                               const uint64_t* kv_lens, const uint64_t* query_lens,
+                               const uint64_t* query_offsets, uint64_t num_seqs,
+                               uint64_t max_query_tokens, uint64_t max_kv_len, uint64_t query_heads,
+                               const float* query, float* output, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Callers of the hot path: copy-on-write and device-side batch metadata.
  *

@@ -124,6 +124,15 @@ struct PrefillParams {
     std::uint32_t split_tiles;
     float* part_o;
     float* part_ml;
+    // Batch launches (num_seqs > 0): workgroup sequence (blockIdx.x / heads)
+    // % num_seqs, whose table is row `seq` of `table` (table_len entries per
+    // row), with seq_kv_lens[seq] tokens of which the last seq_q_lens[seq]
+    // are queries, at rows seq_q_offsets[seq] .. of query/output. qblocks is
+    // then the largest query block count; kv_len bounds every sequence.
+    std::uint32_t num_seqs;
+    const std::uint64_t* seq_kv_lens;
+    const std::uint64_t* seq_q_lens;
+    const std::uint64_t* seq_q_offsets;
 };
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt(n) alone, lgkmcnt(0) alone.
@@ -188,11 +197,30 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int col = lane % 16, quad = lane / 16;
     const std::uint32_t kvh = blockIdx.x % p.heads;
-    const std::uint32_t split = (blockIdx.x / p.heads) % p.splits;
-    const std::uint32_t qb = p.qblocks - 1 - blockIdx.x / p.heads / p.splits;
+    // This workgroup's sequence: the launch's one, or in a batch launch
+    // sequence (blockIdx.x / heads) % num_seqs (heavy query blocks of every
+    // sequence first). All values wave-uniform.
+    std::uint32_t split = 0, qb = 0, kv_len = p.kv_len, tq = p.tq, table_len = p.table_len;
+    const std::uint64_t* table = p.table;
+    const float* query = p.query;
+    float* output = p.output;
+    if (p.num_seqs == 0) {
+        split = (blockIdx.x / p.heads) % p.splits;
+        qb = p.qblocks - 1 - blockIdx.x / p.heads / p.splits;
+    } else {
+        const std::uint32_t seq = (blockIdx.x / p.heads) % p.num_seqs;
+        qb = p.qblocks - 1 - blockIdx.x / p.heads / p.num_seqs;
+        const std::uint64_t kvl = p.seq_kv_lens[seq], ql = p.seq_q_lens[seq], q0 = p.seq_q_offsets[seq];
+        kv_len = static_cast<std::uint32_t>(kvl < p.kv_len ? kvl : p.kv_len);
+        tq = static_cast<std::uint32_t>(ql < kv_len ? ql : kv_len);
+        table = p.table + static_cast<std::uint64_t>(seq) * p.table_len;
+        query = p.query + q0 * p.query_heads * kD;
+        output = p.output + q0 * p.query_heads * kD;
+        if (tq == 0 || static_cast<std::uint64_t>(qb) * kTok >= tq) return;  // uniform
+    }
     const std::uint32_t t0 = qb * kTok;
-    const std::uint32_t t_end = t0 + kTok < p.tq ? t0 + kTok : p.tq;
-    const std::uint32_t past = p.kv_len - p.tq;
+    const std::uint32_t t_end = t0 + kTok < tq ? t0 + kTok : tq;
+    const std::uint32_t past = kv_len - tq;
     const std::uint32_t last_key = past + t_end - 1;
     const std::uint32_t ntiles = last_key / kPfTile + 1;
     // This split's tiles [tile_begin, tile_end). The split holding the tile of
@@ -216,8 +244,8 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     auto stage = [&](std::uint32_t first) {
         for (std::uint32_t i = tid; i < kWin && first + i < npages; i += kPfThreads) {
             const std::uint32_t pg = first + i;
-            const std::uint64_t id = pg < p.table_len ? p.table[pg] : p.num_blocks;
-            const bool ok = id < p.num_blocks && (static_cast<std::uint64_t>(pg) << p.bs_shift) < p.kv_len;
+            const std::uint64_t id = pg < table_len ? table[pg] : p.num_blocks;
+            const bool ok = id < p.num_blocks && (static_cast<std::uint64_t>(pg) << p.bs_shift) < kv_len;
             pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
         }
     };
@@ -231,9 +259,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         const int g = b % kG;
         const std::uint32_t token = t0 + 16 * (b / kG) + col;
         row_token[n] = token;
-        const std::uint32_t tq_safe = token < p.tq ? token : p.tq - 1;
+        const std::uint32_t tq_safe = token < tq ? token : tq - 1;
         const float* src =
-            p.query + (static_cast<std::uint64_t>(tq_safe) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
+            query + (static_cast<std::uint64_t>(tq_safe) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
 #pragma unroll
         for (int kk = 0; kk < kSteps; ++kk) {
             const float4 lo = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8);
@@ -298,7 +326,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         for (int i = 0; i < kDma; ++i) {
             const int e = (i * kPfWaves + wave) * 64 + lane;
             const std::uint32_t key = tile * kPfTile + static_cast<std::uint32_t>(e / kCpr);
-            if (key >= p.kv_len) *reinterpret_cast<uint4*>(reinterpret_cast<char*>(vt) + e * 16) = make_uint4(0, 0, 0, 0);
+            if (key >= kv_len) *reinterpret_cast<uint4*>(reinterpret_cast<char*>(vt) + e * 16) = make_uint4(0, 0, 0, 0);
         }
     };
 
@@ -418,7 +446,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     // t + 1 are issued before tile t is computed; each step waits for its own
     // tile's loads (2 * kDma per thread, issued one step earlier), then a
     // barrier publishes the tile; a second barrier frees the buffer.
-    const bool tail = ntiles * kPfTile > p.kv_len;  // the last tile has keys past kv_len
+    const bool tail = ntiles * kPfTile > kv_len;  // the last tile has keys past kv_len
     // Called at the top of a step, before tile `next` is issued. The barrier
     // first: every wave must be past its reads of the page list for the tiles
     // before `next` (a wave's reads are complete once it has issued that
@@ -475,8 +503,8 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             // One store path for both cases (two would hold the accumulators
             // twice): normalised rows of the output, or unnormalised partials.
             const bool whole = p.splits == 1;
-            const std::uint64_t prow = static_cast<std::uint64_t>(split) * p.tq * p.query_heads + row;
-            float* dst = whole ? p.output + row * kD : p.part_o + prow * kD;
+            const std::uint64_t prow = static_cast<std::uint64_t>(split) * tq * p.query_heads + row;
+            float* dst = whole ? output + row * kD : p.part_o + prow * kD;
             const float sc = whole ? inv : 1.0f;
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
@@ -531,9 +559,12 @@ template <typename E, int kD, int kG>
 int launch_prefill_pass(const PrefillParams& p, hipStream_t s) {
     PrefillParams q = p;
     constexpr unsigned kTok = 16 * (kPfWaves * pf_blocks_per_wave<kD>() / kG);
+    // tq: the query tokens of the sequence, or the most of any sequence of a batch.
     q.qblocks = (p.tq + kTok - 1) / kTok;
-    hipLaunchKernelGGL((paged_prefill_kernel<E, kD, kG>), dim3(q.qblocks * p.heads * p.splits), dim3(kPfThreads), 0,
-                       s, q);
+    const std::uint64_t grid = static_cast<std::uint64_t>(q.qblocks) * p.heads * (p.num_seqs ? p.num_seqs : p.splits);
+    if (grid > 0xffffffffULL) return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: %llu workgroups",
+                                          static_cast<unsigned long long>(grid));
+    hipLaunchKernelGGL((paged_prefill_kernel<E, kD, kG>), dim3(static_cast<unsigned>(grid)), dim3(kPfThreads), 0, s, q);
     return launch_status("paged_prefill_kernel");
 }
 
@@ -725,4 +756,61 @@ extern "C" int kvflux_paged_prefill_split(const void* key_cache, const void* val
     return paged_prefill(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype, block_table,
                          num_table_blocks, kv_len, query_tokens, query_heads, query, output, workspace,
                          workspace_bytes, stream);
+}
+
+extern "C" int kvflux_paged_prefill_batch(const void* key_cache, const void* value_cache, uint64_t num_blocks,
+                                          uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size, int dtype,
+                                          const uint64_t* block_table, uint64_t max_blocks_per_seq,
+                                          const uint64_t* kv_lens, const uint64_t* query_lens,
+                                          const uint64_t* query_offsets, uint64_t num_seqs, uint64_t max_query_tokens,
+                                          uint64_t max_kv_len, uint64_t query_heads, const float* query, float* output,
+                                          void* stream) {
+    if (num_seqs == 0 || max_query_tokens == 0) return KVFLUX_OK;
+    if (dtype_bytes(dtype) == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+    if (!key_cache || !value_cache || !block_table || !kv_lens || !query_lens || !query_offsets || !query ||
+        !output) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill batch: null pointer");
+    }
+    if (num_blocks == 0 || num_kv_heads == 0 || block_size == 0 || head_size == 0 || query_heads == 0 ||
+        query_heads % num_kv_heads != 0 || max_blocks_per_seq == 0) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill batch: invalid shape");
+    }
+    if (max_query_tokens > max_kv_len) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill batch: more queries than tokens");
+    }
+    if (max_blocks_per_seq * block_size < max_kv_len) {
+        return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill batch: table rows shorter than max_kv_len");
+    }
+    if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128 && head_size != 256) ||
+        !is_pow2(block_size) || block_size > 256 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 ||
+        max_kv_len > 0x7fffffffULL || query_heads > 0xffffffffULL || num_seqs > 0xffffffffULL ||
+        max_blocks_per_seq > 0xffffffffULL || num_kv_heads * block_size * head_size * 2 > 0xffffffffULL) {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill batch: shape not handled by the MFMA kernel");
+    }
+    PrefillParams p{};
+    p.key_cache = key_cache;
+    p.value_cache = value_cache;
+    p.num_blocks = num_blocks;
+    p.heads = static_cast<std::uint32_t>(num_kv_heads);
+    std::uint32_t shift = 0;
+    while ((std::uint64_t{1} << shift) < block_size) ++shift;
+    p.bs_shift = shift;
+    p.table = block_table;
+    p.table_len = static_cast<std::uint32_t>(max_blocks_per_seq);
+    p.kv_len = static_cast<std::uint32_t>(max_kv_len);
+    p.tq = static_cast<std::uint32_t>(max_query_tokens);
+    p.query_heads = static_cast<std::uint32_t>(query_heads);
+    p.query = query;
+    p.output = output;
+    p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_size)));
+    p.splits = 1;
+    p.split_tiles = static_cast<std::uint32_t>((max_kv_len + kPfTile - 1) / kPfTile);
+    p.num_seqs = static_cast<std::uint32_t>(num_seqs);
+    p.seq_kv_lens = kv_lens;
+    p.seq_q_lens = query_lens;
+    p.seq_q_offsets = query_offsets;
+    const hipStream_t s = as_stream(stream);
+    const std::uint32_t g = static_cast<std::uint32_t>(query_heads / num_kv_heads);
+    if (dtype == KVFLUX_DTYPE_BF16) return launch_prefill_head_size<PfBf16>(p, head_size, g, s);
+    return launch_prefill_head_size<PfF16>(p, head_size, g, s);
 }

@@ -327,3 +327,60 @@ def test_prefill_small_pages_and_missing_ids(gpu, name, kv_heads, q_heads, head_
     emu = emulate(kh, vh, name, kv_heads, bs, head_size, ref_table, kv_len, q, q_tokens, q_heads, rows)
     sub = got.reshape(q_tokens, q_heads, head_size)[rows]
     assert np.abs(sub - emu).max() < 4e-3
+
+
+BATCH_CASES = [  # name, kv_heads, q_heads, head_size, bs, [(kv_len, q_len), ...]
+    ("BFloat16", 2, 8, 128, 16, [(700, 700), (1500, 1500), (64, 64), (1000, 37), (2049, 2049)]),
+    ("Float16", 1, 5, 64, 4, [(300, 300), (257, 100), (33, 33)]),
+    ("BFloat16", 2, 4, 256, 32, [(400, 400), (1200, 800)]),
+    ("BFloat16", 1, 12, 128, 1, [(200, 200), (150, 1)]),  # group 12 as two passes of 6
+]
+
+
+@pytest.mark.parametrize("name,kv_heads,q_heads,head_size,bs,seqs", BATCH_CASES)
+def test_prefill_batch_matches_single_calls(gpu, name, kv_heads, q_heads, head_size, bs, seqs):
+    """kvflux_paged_prefill_batch: every sequence of the batch, with its own
+    table row, length, query count (whole prompts and trailing chunks) and
+    query offset, gives the same bits as kvflux_paged_prefill on that
+    sequence alone; rows between sequences are untouched; a sampled check
+    against the oracle at 2e-2."""
+    lib = capi.lib()
+    n = len(seqs)
+    width = max((kv + bs - 1) // bs for kv, _ in seqs) + 3
+    blocks = n * width + 5
+    kc, vc, _ = setup_case(name, blocks, kv_heads, bs, head_size, 1, 17 + n)
+    rng = np.random.default_rng(23 + n)
+    order = rng.permutation(blocks).astype(np.uint64)
+    table = np.full((n, width), 2**64 - 1, np.uint64)
+    for i, (kv, _) in enumerate(seqs):
+        npg = (kv + bs - 1) // bs
+        table[i, :npg] = order[i * width:i * width + npg]
+    q_lens = np.array([ql for _, ql in seqs], np.uint64)
+    kv_lens = np.array([kv for kv, _ in seqs], np.uint64)
+    gap = 3  # unused rows between sequences in Q/O
+    offsets = np.concatenate([[0], np.cumsum(q_lens + gap)[:-1]]).astype(np.uint64)
+    rows_total = int(offsets[-1] + q_lens[-1] + gap)
+    row = q_heads * head_size
+    q = oracle.random_elements(0, rows_total * row, oracle.F32, 1, 29 + n)
+    td, qd = buffer_like(table.reshape(-1)), buffer_like(q)
+    kd, ld, od_ = buffer_like(kv_lens), buffer_like(q_lens), buffer_like(offsets)
+    out = buffer_like(np.full(rows_total * row, 555.0, np.float32))
+    assert lib.kvflux_paged_prefill_batch(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, CODES[name], td.ptr,
+                                          width, kd.ptr, ld.ptr, od_.ptr, n, int(q_lens.max()), int(kv_lens.max()),
+                                          q_heads, qd.ptr, out.ptr, None) == 0, capi.last_error()
+    device.synchronize()
+    got = out.download(np.float32).reshape(rows_total, row)
+    used = np.zeros(rows_total, bool)
+    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    for i, (kv, ql) in enumerate(seqs):
+        o0 = int(offsets[i])
+        used[o0:o0 + ql] = True
+        qi = q.reshape(rows_total, row)[o0:o0 + ql].reshape(-1)
+        single = run_prefill(name, kc, vc, blocks, kv_heads, bs, head_size, table[i], kv, qi, ql, q_heads)
+        assert np.array_equal(got[o0:o0 + ql].reshape(-1).view(np.uint32), single.view(np.uint32)), i
+        pick = sorted({0, ql - 1, ql // 2})
+        exp = oracle.paged_attention_rows(kh, vh, kv_heads, bs, head_size, CODES[name], np.tile(table[i], len(pick)),
+                                          width, np.array([kv - ql + t + 1 for t in pick], np.uint64),
+                                          qi.reshape(ql, row)[pick].reshape(-1), q_heads, threads=8)
+        assert np.abs(got[o0:o0 + ql][pick].reshape(-1) - exp).max() < 2e-2
+    assert np.all(got[~used] == 555.0)
