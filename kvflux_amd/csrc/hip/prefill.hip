@@ -346,11 +346,13 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 #pragma unroll
         for (int n = 0; n < kPfNt; ++n) acc[dt][n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     pf_f32x4_t lsum[kPfNt];
-    float nref[kPfNt];  // minus the row's reference point (equal in the four quads of a column)
+    // Minus the row's reference point, in all four accumulator lanes (the
+    // seed of every QK^T chain; equal in the four quads of a column).
+    pf_f32x4_t nref[kPfNt];
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
         lsum[n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        nref[n] = 0.0f;
+        nref[n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     bool have_ref = false;
     const Vec ones = __builtin_bit_cast(Vec, make_uint4(M::kOnes, M::kOnes, M::kOnes, M::kOnes));
@@ -363,22 +365,25 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             if (k0 > last_key) break;  // uniform
             pf_f32x4_t s[2][kPfNt];
             set_priority<1>();
+            {
+                Vec a[kSteps][2];
 #pragma unroll
-            for (int kt2 = 0; kt2 < 2; ++kt2) {
-                Vec a[kSteps];
+                for (int kk = 0; kk < kSteps; ++kk)
 #pragma unroll
-                for (int kk = 0; kk < kSteps; ++kk) {
-                    a[kk] = __builtin_bit_cast(
-                        Vec, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(kt) +
-                                                             (32 * h + 16 * kt2) * kRowBytes + (k_read0 ^ (kk << 6))));
-                }
+                    for (int kt2 = 0; kt2 < 2; ++kt2)
+                        a[kk][kt2] = __builtin_bit_cast(
+                            Vec, *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(kt) +
+                                                                 (32 * h + 16 * kt2) * kRowBytes + (k_read0 ^ (kk << 6))));
 #pragma unroll
-                for (int n = 0; n < kPfNt; ++n) {
-                    pf_f32x4_t x = pf_f32x4_t{nref[n], nref[n], nref[n], nref[n]};
+                for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
-                    for (int kk = 0; kk < kSteps; ++kk) x = M::mma(a[kk], qb_op[n][kk], x);
-                    s[kt2][n] = x;
-                }
+                    for (int n = 0; n < kPfNt; ++n) s[kt2][n] = nref[n];
+#pragma unroll
+                for (int kk = 0; kk < kSteps; ++kk)
+#pragma unroll
+                    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+                        for (int n = 0; n < kPfNt; ++n) s[kt2][n] = M::mma(a[kk][kt2], qb_op[n][kk], s[kt2][n]);
             }
             set_priority<0>();
             if (k0 + 31 > min_limit) {
@@ -391,19 +396,25 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                         for (int r = 0; r < 4; ++r) s[kt2][n][r] = 16 * kt2 + r > room ? -INFINITY : s[kt2][n][r];
                 }
             }
-            float tmax[kPfNt];
+            // The wave rescales when some row's maximum exceeds its reference
+            // by 2^kLazy: a lane's own maximum over its scores of the row
+            // decides that (the row maximum, over the four quads, is needed
+            // only inside the rare branch). A lane whose own maximum passes
+            // while its row maximum is NaN enters with a zero shift for that
+            // row, which changes nothing.
+            float lmax[kPfNt];
             bool grow = !have_ref;
 #pragma unroll
             for (int n = 0; n < kPfNt; ++n) {
-                tmax[n] = max_across_quads(max3(max3(s[0][n][0], s[0][n][1], s[0][n][2]),
-                                                max3(s[0][n][3], s[1][n][0], s[1][n][1]),
-                                                max3(s[1][n][2], s[1][n][3], -INFINITY)));
-                grow |= tmax[n] > kLazy;
+                lmax[n] = max3(max3(s[0][n][0], s[0][n][1], s[0][n][2]), max3(s[0][n][3], s[1][n][0], s[1][n][1]),
+                               max3(s[1][n][2], s[1][n][3], -INFINITY));
+                grow |= lmax[n] > kLazy;
             }
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {
 #pragma unroll
                 for (int n = 0; n < kPfNt; ++n) {
-                    const float shift = !have_ref || tmax[n] > kLazy ? tmax[n] : 0.0f;
+                    const float tmax = max_across_quads(lmax[n]);
+                    const float shift = !have_ref || tmax > kLazy ? tmax : 0.0f;
                     const float alpha = __builtin_amdgcn_exp2f(fminf(-shift, 0.0f));
                     nref[n] -= shift;
                     lsum[n] *= alpha;
@@ -512,7 +523,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                     make_float4(acc[dt][n][0] * sc, acc[dt][n][1] * sc, acc[dt][n][2] * sc, acc[dt][n][3] * sc);
             }
             // An empty split leaves l = 0; the combine skips it.
-            if (!whole && quad == 0) *reinterpret_cast<float2*>(p.part_ml + 2 * prow) = make_float2(-nref[n], l);
+            if (!whole && quad == 0) *reinterpret_cast<float2*>(p.part_ml + 2 * prow) = make_float2(-nref[n][0], l);
         }
     }
 }
