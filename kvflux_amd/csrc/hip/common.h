@@ -59,8 +59,9 @@ struct alignas(8) V8 { std::uint32_t w[2]; };
 
 // Non-temporal load / store of one raw vector (16, 8, 4 or 2 bytes): the
 // `nt` form of global_load / global_store, for data touched once (streamed
-// pages). Measured on MI355X, a read stream of random 32 KiB blocks runs at
-// 7.0 TB/s with the hint against 6.2 TB/s without. Loads whose 128-byte
+// pages). Measured on MI355X, a read-only stream of random 32 KiB blocks
+// gains 0.5-1.5% with the hint; a copy gains more (the batch gather: 448 ->
+// 415 us with non-temporal loads and stores). Loads whose 128-byte
 // lines are completed by other instructions of the same wave must not use
 // it (the line may be gone before the second half is read).
 template <typename Vec>
