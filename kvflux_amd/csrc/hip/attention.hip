@@ -1059,7 +1059,12 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
 
         const bool single = lens[cur.row] <= chunk_tokens || p.max_chunks <= 1;
         const std::uint32_t qh0 = cur.kvh * p.q_group + p.q_first;
-        for (int idx = tid; idx < kG * kD; idx += kThreads) {
+        // The thread index is opaque here, so the epilogue's addresses are
+        // formed per item rather than hoisted and held through the tile loop
+        // (at D = 128, G = 6 and 7 with FP16 they would not fit the registers).
+        int first_idx = tid;
+        asm volatile("" : "+v"(first_idx));
+        for (int idx = first_idx; idx < kG * kD; idx += kThreads) {
             const int g = idx / kD, d = idx % kD;
             float m = -INFINITY;
 #pragma unroll
