@@ -520,7 +520,8 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 }
 
 // ---------------------------------------------------------------- block_size 16 decode
-// Hot path for pages of 16 (to 128) tokens, 16-bit caches, head_size 64/128:
+// Hot path for head_size 64/128: 16-bit caches with pages of 1 to 128 tokens,
+// FP32 caches with pages of 16 to 128 tokens:
 //  * persistent workgroups walk a plan of (row, chunk, kv head) items built
 //    in LDS from the row lengths (exclusive prefix of chunk counts), so no
 //    workgroup is launched for an empty chunk and consecutive items read the
@@ -547,7 +548,12 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 //    wave's own LDS copy of the tile through the transposing ds_read_tr16_b64,
 //    and P^T (the B operand) is exactly the four weights each score lane
 //    holds (tokens 4*quad .. 4*quad+3 of its column);
-//  * K and V of the next tile are in flight while the current one is computed.
+//  * K and V of the next tile are in flight while the current one is computed;
+//  * FP32 caches: QK^T is kD/4 v_mfma_f32_16x16x4_f32 on K and Q as they
+//    are, and P*V 4 * kD/16 of them on V and the FP32 weights; the dims and
+//    tokens each lane takes are ordered so that K, V and Q are read with
+//    straight 16-byte loads (no splits, no LDS copy of V): 2.40 against
+//    3.03 ms on the VALU split kernel for 128 rows of U[1024, 32768] tokens.
 // V tile in LDS: row t (token) holds kD 16-bit values as kD/8 chunks of 16
 // bytes; chunk c of row t is stored at slot c ^ ((kD/64) * (t % 8)), which
 // makes both the row-wise 16-byte writes and the transposing 8-byte reads
@@ -601,17 +607,22 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 // take one wave-uniform page.
 template <typename E, int kD, int kG, bool kSmall>
 __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p) {
-    using M = Mfma<E>;
+    // FP32 caches: QK^T and P*V on v_mfma_f32_16x16x4_f32 with FP32 K, V, Q
+    // and weights as they are (no splits, no LDS staging of V).
+    constexpr bool kF32 = std::is_same<E, F32>::value;
+    static_assert(!(kF32 && kSmall), "FP32 caches take pages of 16 tokens or more");
+    using M = Mfma<typename std::conditional<kF32, Bf16, E>::type>;
     using Vec = typename M::Vec;
     using T = typename E::Storage;
     constexpr int kBs = 16;
+    constexpr int kF32Chunks = kD / 16;     // FP32: 16-byte K (and V) loads per lane per tile
     constexpr int kSteps = kD / 32;         // QK MFMAs per tile (32 dims each)
     constexpr int kDt = kD / 16;            // P*V MFMAs per tile (16 dims each)
     constexpr int kCpr = kD / 8;            // 16-byte chunks per token row
     constexpr int kVLoads = kD / 32;        // 16-byte V chunks per lane per tile
     constexpr int kRowStep = 64 / kCpr;     // token rows covered by one wave-wide load
     constexpr int kSwz = kCpr / 8;          // LDS slot swizzle multiplier
-    constexpr int kSets = 3 * kG <= 16 ? 1 : 2;
+    constexpr int kSets = kF32 || 3 * kG <= 16 ? 1 : 2;
     constexpr int kRowBytes = kD * 2;
     constexpr int kQPer = (kG * kD + kThreads - 1) / kThreads;
     static_assert(kRowStep * kVLoads == kBs, "V tile covers 16 tokens");
@@ -630,8 +641,11 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     __shared__ std::uint32_t plan[kPlanRows + 1];
     __shared__ std::uint32_t lens[kPlanRows];
     __shared__ std::uint32_t scan[kThreads];
-    __shared__ __attribute__((aligned(16))) std::uint16_t qsplit[2][3 * kG * kD];
-    __shared__ __attribute__((aligned(16))) std::uint16_t vtile[kWaves][kBs * kD];
+    // 16-bit caches: Q split in three 16-bit parts; FP32: Q as floats (two
+    // 16-bit slots each). V tiles are staged for the transposing reads of the
+    // 16-bit path only.
+    __shared__ __attribute__((aligned(16))) std::uint16_t qsplit[2][(kF32 ? 2 : 3) * kG * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t vtile[kWaves][kF32 ? 8 : kBs * kD];
     __shared__ __attribute__((aligned(16))) float reduce[kWaves * kG * kD];
     __shared__ float wstats[kWaves][2 * kG];
 
@@ -783,11 +797,15 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             const int idx = tid + kThreads * i;
             if (idx < kG * kD) {
                 const int g = idx / kD, d = idx % kD;
-                float rest;
                 const float x = q[i] * p.scale_log2;
-                qsplit[s][(0 * kG + g) * kD + d] = M::split(x, &rest);
-                qsplit[s][(1 * kG + g) * kD + d] = M::split(rest, &rest);
-                qsplit[s][(2 * kG + g) * kD + d] = M::split(rest, &rest);
+                if constexpr (kF32) {
+                    reinterpret_cast<float*>(qsplit[s])[g * kD + d] = x;
+                } else {
+                    float rest;
+                    qsplit[s][(0 * kG + g) * kD + d] = M::split(x, &rest);
+                    qsplit[s][(1 * kG + g) * kD + d] = M::split(rest, &rest);
+                    qsplit[s][(2 * kG + g) * kD + d] = M::split(rest, &rest);
+                }
             }
         }
     };
@@ -798,11 +816,26 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     };
 
     struct Tile {
-        uint4 k[kSteps];
-        uint4 v[kVLoads];
+        uint4 k[kF32 ? kF32Chunks : kSteps];
+        uint4 v[kF32 ? kF32Chunks : kVLoads];
     };
     auto load = [&](std::uint64_t off, std::uint32_t kvh, Tile& b) {
         const std::uint64_t base = (off == kNoPage ? 0 : off) + kvh * head_stride;
+        if constexpr (kF32) {
+            // K: lane (quad, col) takes token col, 16-byte chunks 4m + quad
+            // (two loads complete each 128-byte line). V: token 4 * quad + kk,
+            // chunks 16 * mm + col (whole lines per load, streamed).
+            const T* kb = kc + base + col * kD + quad * 4;
+            const T* vb = vc + base + (4 * quad) * kD + col * 4;
+#pragma unroll
+            for (int m = 0; m < kF32Chunks; ++m) b.k[m] = *reinterpret_cast<const uint4*>(kb + 16 * m);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int mm = 0; mm < kD / 64; ++mm)
+                    b.v[kk * (kD / 64) + mm] = stream_load(reinterpret_cast<const uint4*>(vb + kk * kD + 64 * mm));
+            return;
+        }
         const T* kb = kc + base + k_lane;
         const T* vb = vc + base + v_lane;
 #pragma unroll
@@ -846,7 +879,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     constexpr float kLazy = 8.0f;
     float run_max, run_sum;
     f32x4_t acc[kSets][kDt];
-    Vec qb[kSets][kSteps];
+    Vec qb[kSets][kF32 ? 1 : kSteps];
+    float qf[kF32 ? kD / 4 : 1];  // FP32: Q of head col, dims 16 * (kk / 4) + 4 * quad + kk % 4
 
     // consume(): V of the tile into the wave's LDS slot and the QK^T MFMAs;
     // after it the tile's registers are free for the next load.
@@ -857,38 +891,50 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     auto consume = [&](std::uint32_t valid, const Tile& b) -> Scores {
         Scores out;
         out.valid = valid;
+        if constexpr (kF32) {
+            // S^T = K Q^T over dims: MFMA kk takes, in lane (quad, col), dim
+            // 16 * (kk / 4) + 4 * quad + kk % 4 of token col (K) and of head
+            // col (Q, in qf[kk]); the dim order does not change the sum.
+            out.s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            out.s1 = out.s0;
 #pragma unroll
-        for (int i = 0; i < kVLoads; ++i) *reinterpret_cast<uint4*>(my_tile + v_store[i]) = b.v[i];
-        if (valid < kBs) {  // rows past the end read as zero (0 * NaN would poison P*V)
+            for (int m = 0; m < kF32Chunks; ++m) {
+                const float kx[4] = {__uint_as_float(b.k[m].x), __uint_as_float(b.k[m].y), __uint_as_float(b.k[m].z),
+                                     __uint_as_float(b.k[m].w)};
 #pragma unroll
-            for (int i = 0; i < kVLoads; ++i) {
-                if (static_cast<std::uint32_t>(lane / kCpr + i * kRowStep) >= valid)
-                    *reinterpret_cast<uint4*>(my_tile + v_store[i]) = make_uint4(0, 0, 0, 0);
+                for (int j = 0; j < 4; ++j)
+                    out.s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[j], qf[4 * m + j], out.s0, 0, 0, 0);
             }
-        }
-        out.s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        out.s1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        } else {
 #pragma unroll
-        for (int kk = 0; kk < kSteps; ++kk) {
-            const Vec a = __builtin_bit_cast(Vec, b.k[kk]);
-            out.s0 = M::mma(a, qb[0][kk], out.s0);
-            if constexpr (kSets == 2) out.s1 = M::mma(a, qb[1][kk], out.s1);
+            for (int i = 0; i < kVLoads; ++i) *reinterpret_cast<uint4*>(my_tile + v_store[i]) = b.v[i];
+            if (valid < kBs) {  // rows past the end read as zero (0 * NaN would poison P*V)
+#pragma unroll
+                for (int i = 0; i < kVLoads; ++i) {
+                    if (static_cast<std::uint32_t>(lane / kCpr + i * kRowStep) >= valid)
+                        *reinterpret_cast<uint4*>(my_tile + v_store[i]) = make_uint4(0, 0, 0, 0);
+                }
+            }
+            out.s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            out.s1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < kSteps; ++kk) {
+                const Vec a = __builtin_bit_cast(Vec, b.k[kk]);
+                out.s0 = M::mma(a, qb[0][kk], out.s0);
+                if constexpr (kSets == 2) out.s1 = M::mma(a, qb[1][kk], out.s1);
+            }
         }
         return out;
     };
 
     // finish(): online softmax of the tile's scores and the P*V MFMAs.
-    auto finish = [&](const Scores& in) {
+    auto finish_f32 = [&](const Scores& in, const Tile& b) {
         const std::uint32_t valid = in.valid;
         // Lane (quad, col < kG) holds the scores of tokens 4*quad+r, head col.
         float sc[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            if constexpr (kSets == 1) {
-                sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + row_shl<2 * kG>(in.s0[r]);
-            } else {
-                sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + in.s1[r];
-            }
+            sc[r] = in.s0[r];
             if (valid < kBs && static_cast<std::uint32_t>(quad * 4 + r) >= valid) sc[r] = -INFINITY;
         }
         float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
@@ -897,49 +943,103 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         const bool grow = tmax > run_max + kLazy;
         const float old_max = run_max;
         if (grow) run_max = tmax;
-        const float ref = run_max == -INFINITY ? 0.0f : run_max;  // exp2(-inf - ref) = 0
+        const float ref = run_max == -INFINITY ? 0.0f : run_max;
         const float alpha = grow ? __builtin_amdgcn_exp2f(old_max - ref) : 1.0f;
-
-        // Weights, split into three 16-bit parts and routed to the columns
-        // (split, head): lane col < kG keeps hi, the mid and lo parts move kG
-        // and 2*kG lanes up the row.
-        std::uint32_t w0[4], w1[4];
+        float pr[4];
         float psum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float pr = __builtin_amdgcn_exp2f(sc[r] - ref);
-            psum += pr;
-            std::uint32_t whi, wmid, wlo;
-            M::split3(pr, whi, wmid, wlo);
-            w0[r] = route<kG, kSets>(whi, wmid, wlo, col);
-            if constexpr (kSets == 2) w1[r] = wlo;
+            pr[r] = __builtin_amdgcn_exp2f(sc[r] - ref);
+            psum += pr[r];
         }
         run_sum = run_sum * alpha + psum;
-
-        // Rescale the columns whose reference point moved (never needed while
-        // nothing has been accumulated yet).
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(col < kG && grow && old_max != -INFINITY) != 0, 0)) {
-            const float a0 = __uint_as_float(route<kG, kSets>(__float_as_uint(alpha), __float_as_uint(alpha),
-                                                              __float_as_uint(alpha), col));
 #pragma unroll
-            for (int dt = 0; dt < kDt; ++dt) acc[0][dt] *= a0;
-            if constexpr (kSets == 2) {
+            for (int dt = 0; dt < kDt; ++dt) scale_in_place(acc[0][dt], alpha);
+        }
+        // O^T += V^T P^T over tokens: MFMA kk takes token 4 * quad + kk in
+        // lane (quad, col), the weight the lane holds in pr[kk]; block dt of
+        // O^T is dims 64 * (dt / 4) + 4 * i + dt % 4, i = 0..15. V rows of
+        // tokens past the end read as zero (0 * NaN would poison P*V).
 #pragma unroll
-                for (int dt = 0; dt < kDt; ++dt) acc[1][dt] *= alpha;
+        for (int kk = 0; kk < 4; ++kk) {
+            const bool live = static_cast<std::uint32_t>(4 * quad + kk) < valid;
+#pragma unroll
+            for (int mm = 0; mm < kD / 64; ++mm) {
+                const uint4 w = b.v[kk * (kD / 64) + mm];
+                const float vx[4] = {live ? __uint_as_float(w.x) : 0.0f, live ? __uint_as_float(w.y) : 0.0f,
+                                     live ? __uint_as_float(w.z) : 0.0f, live ? __uint_as_float(w.w) : 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[0][4 * mm + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vx[j], pr[kk], acc[0][4 * mm + j], 0, 0, 0);
             }
         }
+    };
 
-        const i16x4_t pb0 = M::pack(w0);
-        i16x4_t pb1;
-        if constexpr (kSets == 2) pb1 = M::pack(w1);
+    auto finish = [&](const Scores& in) {
+        if constexpr (!kF32) {
+            const std::uint32_t valid = in.valid;
+            // Lane (quad, col < kG) holds the scores of tokens 4*quad+r, head col.
+            float sc[4];
 #pragma unroll
-        for (int dt = 0; dt < kDt; ++dt) {
-            lds_i16x4_t* src = (lds_i16x4_t*)((__attribute__((address_space(3))) char*)(
-                                       (__attribute__((address_space(3))) std::uint16_t*)vtile[wave]) +
-                                   (v_read ^ (dt << 5)));
-            const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(src);
-            acc[0][dt] = M::mma16(va, pb0, acc[0][dt]);
-            if constexpr (kSets == 2) acc[1][dt] = M::mma16(va, pb1, acc[1][dt]);
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (kSets == 1) {
+                    sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + row_shl<2 * kG>(in.s0[r]);
+                } else {
+                    sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + in.s1[r];
+                }
+                if (valid < kBs && static_cast<std::uint32_t>(quad * 4 + r) >= valid) sc[r] = -INFINITY;
+            }
+            float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            tmax = fmaxf(tmax, swizzle_xor16(tmax));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const bool grow = tmax > run_max + kLazy;
+            const float old_max = run_max;
+            if (grow) run_max = tmax;
+            const float ref = run_max == -INFINITY ? 0.0f : run_max;  // exp2(-inf - ref) = 0
+            const float alpha = grow ? __builtin_amdgcn_exp2f(old_max - ref) : 1.0f;
+
+            // Weights, split into three 16-bit parts and routed to the columns
+            // (split, head): lane col < kG keeps hi, the mid and lo parts move kG
+            // and 2*kG lanes up the row.
+            std::uint32_t w0[4], w1[4];
+            float psum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pr = __builtin_amdgcn_exp2f(sc[r] - ref);
+                psum += pr;
+                std::uint32_t whi, wmid, wlo;
+                M::split3(pr, whi, wmid, wlo);
+                w0[r] = route<kG, kSets>(whi, wmid, wlo, col);
+                if constexpr (kSets == 2) w1[r] = wlo;
+            }
+            run_sum = run_sum * alpha + psum;
+
+            // Rescale the columns whose reference point moved (never needed while
+            // nothing has been accumulated yet).
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(col < kG && grow && old_max != -INFINITY) != 0, 0)) {
+                const float a0 = __uint_as_float(route<kG, kSets>(__float_as_uint(alpha), __float_as_uint(alpha),
+                                                                  __float_as_uint(alpha), col));
+#pragma unroll
+                for (int dt = 0; dt < kDt; ++dt) acc[0][dt] *= a0;
+                if constexpr (kSets == 2) {
+#pragma unroll
+                    for (int dt = 0; dt < kDt; ++dt) acc[1][dt] *= alpha;
+                }
+            }
+
+            const i16x4_t pb0 = M::pack(w0);
+            i16x4_t pb1;
+            if constexpr (kSets == 2) pb1 = M::pack(w1);
+#pragma unroll
+            for (int dt = 0; dt < kDt; ++dt) {
+                lds_i16x4_t* src = (lds_i16x4_t*)((__attribute__((address_space(3))) char*)(
+                                           (__attribute__((address_space(3))) std::uint16_t*)vtile[wave]) +
+                                       (v_read ^ (dt << 5)));
+                const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(src);
+                acc[0][dt] = M::mma16(va, pb0, acc[0][dt]);
+                if constexpr (kSets == 2) acc[1][dt] = M::mma16(va, pb1, acc[1][dt]);
+            }
         }
     };
 
@@ -974,8 +1074,20 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         float nq[kQPer];
         fetch_query(nxt, nq);
 
+        if constexpr (kF32) {
+            const float* qs = reinterpret_cast<const float*>(qsplit[sel]) + (col < kG ? col : 0) * kD + 4 * quad;
+#pragma unroll
+            for (int m = 0; m < kF32Chunks; ++m) {
+                const float4 x = *reinterpret_cast<const float4*>(qs + 16 * m);
+                qf[4 * m] = col < kG ? x.x : 0.0f;
+                qf[4 * m + 1] = col < kG ? x.y : 0.0f;
+                qf[4 * m + 2] = col < kG ? x.z : 0.0f;
+                qf[4 * m + 3] = col < kG ? x.w : 0.0f;
+            }
+        }
         // B operands from the split table: column -> (split, head). Columns
         // past the last split only feed output columns that are never read.
+        if constexpr (!kF32)
 #pragma unroll
         for (int m = 0; m < kSets; ++m) {
             int split = col / kG, g = col % kG;
@@ -1020,15 +1132,26 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             }
         };
         // Two tiles per step, unrolled once more: a full unroll of 64 tiles
-        // would spill.
+        // would spill. FP32 keeps V in the tile's registers until P*V, so a
+        // buffer is reloaded after its tile is finished.
+        if constexpr (kF32) {
+#pragma unroll 1
+            for (int j = 0; j < per_wave; j += 2) {
+                finish_f32(consume(valid_of(j), buf0), buf0);
+                issue(j + 2, buf0);
+                finish_f32(consume(valid_of(j + 1), buf1), buf1);
+                issue(j + 3, buf1);
+            }
+        } else {
 #pragma unroll 2
-        for (int j = 0; j < per_wave; j += 2) {
-            const Scores s0 = consume(valid_of(j), buf0);
-            issue(j + 2, buf0);
-            finish(s0);
-            const Scores s1 = consume(valid_of(j + 1), buf1);
-            issue(j + 3, buf1);
-            finish(s1);
+            for (int j = 0; j < per_wave; j += 2) {
+                const Scores s0 = consume(valid_of(j), buf0);
+                issue(j + 2, buf0);
+                finish(s0);
+                const Scores s1 = consume(valid_of(j + 1), buf1);
+                issue(j + 3, buf1);
+                finish(s1);
+            }
         }
         if (has_next) stage_query(nq, sel ^ 1);
 
@@ -1040,20 +1163,33 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
             wstats[wave][2 * lane] = run_max;
             wstats[wave][2 * lane + 1] = run_sum;
         }
+        if constexpr (kF32) {
+            // acc[0][4 * mm + j][r] is dim 64 * mm + 16 * quad + 4 * r + j of head col.
 #pragma unroll
-        for (int dt = 0; dt < kDt; ++dt) {
-            float4 o;
-            float* op = reinterpret_cast<float*>(&o);
+            for (int mm = 0; mm < kD / 64; ++mm)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float x = acc[0][dt][r];
-                if constexpr (kSets == 1) {
-                    op[r] = x + row_shl<kG>(x) + row_shl<2 * kG>(x);
-                } else {
-                    op[r] = x + row_shl<kG>(x) + acc[1][dt][r];
+                for (int r = 0; r < 4; ++r) {
+                    const float4 o = make_float4(acc[0][4 * mm][r], acc[0][4 * mm + 1][r], acc[0][4 * mm + 2][r],
+                                                 acc[0][4 * mm + 3][r]);
+                    if (col < kG)
+                        *reinterpret_cast<float4*>(reduce + (wave * kG + col) * kD + 64 * mm + 16 * quad + 4 * r) = o;
                 }
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < kDt; ++dt) {
+                float4 o;
+                float* op = reinterpret_cast<float*>(&o);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float x = acc[0][dt][r];
+                    if constexpr (kSets == 1) {
+                        op[r] = x + row_shl<kG>(x) + row_shl<2 * kG>(x);
+                    } else {
+                        op[r] = x + row_shl<kG>(x) + acc[1][dt][r];
+                    }
+                }
+                if (col < kG) *reinterpret_cast<float4*>(reduce + (wave * kG + col) * kD + dt * 16 + quad * 4) = o;
             }
-            if (col < kG) *reinterpret_cast<float4*>(reduce + (wave * kG + col) * kD + dt * 16 + quad * 4) = o;
         }
         __syncthreads();
 
@@ -1349,7 +1485,7 @@ inline int plan_fallback(std::uint64_t group, std::uint64_t max_chunks, Plan* pl
 template <typename E, int kD>
 int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::uint64_t max_chunks,
                Plan* plan) {
-    if constexpr (!std::is_same<E, F32>::value && (kD == 64 || kD == 128)) {
+    if constexpr (kD == 64 || kD == 128) {
         // The kernel counts work items in 32 bits (at most 512-token chunks);
         // rows <= kPlanRows keeps the product below 2^51.
         const std::uint32_t bs = p.block_size.divisor;
@@ -1371,8 +1507,14 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             // page addresses of larger groups exceed the registers).
             if (small && kD == 128 && sub > kSmallMaxGroup128) return plan_fallback(group, max_chunks, plan);
             int slots = 0;
-            const int status = small ? resident_slots_for<E, kD, true>(sub, &slots)
-                                     : resident_slots_for<E, kD, false>(sub, &slots);
+            int status = KVFLUX_OK;
+            if constexpr (std::is_same<E, F32>::value) {
+                // FP32 caches: pages of 16 tokens or more (FP32 MFMA path).
+                if (small) return plan_fallback(group, max_chunks, plan);
+                status = resident_slots_for<E, kD, false>(sub, &slots);
+            } else {
+                status = small ? resident_slots_for<E, kD, true>(sub, &slots) : resident_slots_for<E, kD, false>(sub, &slots);
+            }
             if (status != KVFLUX_OK) return status;
             // Work item size: the largest chunk (up to 4096 tokens, less for
             // small pages) that still gives at least 8 items per resident
@@ -1468,7 +1610,9 @@ template <typename E, int kD, int kG>
 int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
     p.row_base = 0;
     if (plan.small) {
-        if constexpr (kD != 128 || kG <= static_cast<int>(kSmallMaxGroup128)) {
+        if constexpr (std::is_same<E, F32>::value) {
+            return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: FP32 caches with pages under 16 tokens");
+        } else if constexpr (kD != 128 || kG <= static_cast<int>(kSmallMaxGroup128)) {
             hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, true>), dim3(plan.grid), dim3(kThreads), 0, s, p);
         } else {
             return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %d", kG);
@@ -1521,11 +1665,8 @@ int run_plan(Params p, const Plan& plan, std::uint64_t rows, std::uint64_t head_
              hipStream_t s) {
     switch (plan.family) {
     case Family::Bs16:
-        if constexpr (!std::is_same<E, F32>::value) {
-            if (head_dim == 64) return run_bs16<E, 64>(p, plan, s);
-            return run_bs16<E, 128>(p, plan, s);
-        }
-        break;
+        if (head_dim == 64) return run_bs16<E, 64>(p, plan, s);
+        return run_bs16<E, 128>(p, plan, s);
     case Family::Split:
         if (head_dim == 64) return run_split<E, 64>(p, rows, group, s);
         if (head_dim == 128) return run_split<E, 128>(p, rows, group, s);

@@ -81,6 +81,13 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("Float16", 1, 12, 64, [5, 1030]),
     ("BFloat16", 2, 20, 128, [300, 1111]),
     ("BFloat16", 1, 11, 64, [1, 900]),
+    # FP32 caches on the FP32-MFMA path of the block-size-16 kernel
+    ("Float32", 1, 8, 64, [1, 17, 530, 1100]),
+    ("Float32", 3, 3, 128, [100, 513]),
+    ("Float32", 1, 5, 64, [4, 513, 1200]),
+    ("Float32", 2, 12, 128, [9, 600, 1500]),
+    ("Float32", 1, 7, 128, [2, 777, 2100]),
+    ("Float32", 2, 32, 128, [15, 640, 1700]),
 ]
 
 
@@ -274,6 +281,8 @@ ITEM_CASES = [  # name, head_size, rows, max_len, query heads (2 kv heads)
     ("BFloat16", 64, 256, 16384, 8),
     ("BFloat16", 128, 128, 32768, 16),
     ("BFloat16", 128, 64, 32768, 32),
+    ("Float32", 128, 128, 16384, 8),
+    ("Float32", 64, 128, 8192, 16),
 ]
 
 
@@ -290,8 +299,8 @@ def test_decode_work_item_sizes(gpu, name, head_size, rows, max_len, q_heads):
     are bit-identical."""
     lib = capi.lib()
     H, Hq, bs, P = 2, q_heads, 16, 4096
-    code = DTYPES[name][0]
-    esize = 2
+    code, host = DTYPES[name]
+    esize = np.dtype(host).itemsize
     page = H * bs * head_size
     kc = device.DeviceBuffer(P * page * esize)
     vc = device.DeviceBuffer(P * page * esize)
@@ -326,7 +335,7 @@ def test_decode_work_item_sizes(gpu, name, head_size, rows, max_len, q_heads):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     edge_rows = [int(np.flatnonzero(lens == L)[0]) for L in sorted(set(edges))]
     sample = np.array(sorted(set(edge_rows) | set(rng.choice(rows, 8, replace=False).tolist())))
-    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    kh, vh = kc.download(host), vc.download(host)
     exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table[sample].reshape(-1), width,
                                       lens[sample], q.reshape(rows, -1)[sample].reshape(-1), Hq, threads=8)
     assert np.abs(got[sample].reshape(-1) - exp).max() < TOL
@@ -344,6 +353,9 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
     ("Float16", 8, 64, 1, 8),
     ("BFloat16", 8, 128, 1, 6),   # group 6 at head_size 128: small pages stay on the split kernel
     ("BFloat16", 4, 64, 4, 28),   # group 7 at head_size 64 on the small-page kernel
+    ("Float32", 32, 128, 2, 8),
+    ("Float32", 64, 64, 2, 12),
+    ("Float32", 8, 128, 2, 8),    # FP32 with pages under 16 tokens stays on the split kernel
 ]
 
 
@@ -358,10 +370,10 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     Matches the oracle at 1e-5, bit-identical on repeat."""
     lib = capi.lib()
     P = 512
-    code = DTYPES[name][0]
+    code, host = DTYPES[name]
     page = H * bs * head_size
-    kc = device.DeviceBuffer(P * page * 2)
-    vc = device.DeviceBuffer(P * page * 2)
+    kc = device.DeviceBuffer(P * page * np.dtype(host).itemsize)
+    vc = device.DeviceBuffer(P * page * np.dtype(host).itemsize)
     device.fill_random(kc.ptr, P * page, code, 1, 41)
     device.fill_random(vc.ptr, P * page, code, 1, 42)
     rng = np.random.default_rng(bs * 7 + Hq)
@@ -387,7 +399,7 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
         device.synchronize()
         outs.append(od.download(np.float32))
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
-    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    kh, vh = kc.download(host), vc.download(host)
     exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table.reshape(-1), width, lens, q, Hq,
                                       threads=8)
     assert np.abs(outs[0] - exp).max() < TOL
