@@ -129,15 +129,16 @@ def test_shared_prefix_rows(gpu, v2):
     assert np.abs(od.download(np.float32) - exp).max() < TOL
 
 
-@pytest.mark.parametrize("q_tokens", [1, 9, 37])
-def test_causal_trailing_queries_exact(gpu, v2, q_tokens):
-    pool, storage, seqs, _ = build_batch(v2, "BFloat16", 2, 128, [700], 80, 11)
+@pytest.mark.parametrize("name,q_tokens", [("BFloat16", 1), ("BFloat16", 9), ("BFloat16", 37),
+                                           ("Float32", 1), ("Float32", 37), ("Float16", 9)])
+def test_causal_trailing_queries_exact(gpu, v2, name, q_tokens):
+    pool, storage, seqs, _ = build_batch(v2, name, 2, 128, [700], 80, 11)
     seq = seqs[0]
     q = oracle.random_elements(0, q_tokens * 8 * 128, oracle.F32, 1, q_tokens)
     qd, od = buffer_like(q), buffer_like(np.zeros(q.size, np.float32))
     v2.paged_attention(storage, seq, qd.ptr, od.ptr, q_tokens, 8, v2.AttentionPrecision.Exact)
-    kc, vc = host_cache(storage, "BFloat16")
-    exp = oracle.paged_attention_causal(kc, vc, 2, 16, 128, oracle.BF16,
+    kc, vc = host_cache(storage, name)
+    exp = oracle.paged_attention_causal(kc, vc, 2, 16, 128, DTYPES[name][0],
                                         v2.build_read_block_table(seq), 700, q, q_tokens, 8, threads=8)
     assert np.abs(od.download(np.float32) - exp).max() < TOL
 

@@ -73,10 +73,11 @@ def test_noalloc_matches_workspace_entry(gpu, name, H, Hq, head_size):
 
 
 def test_noalloc_rejects_partials_beyond_the_scratch(gpu):
-    """FP32 caches run on the split kernel with 512-token items: 256 rows of
-    64K tokens at 32 query heads need 545 MB of partials. The call fails on
-    the host with KVFLUX_ERR_UNSUPPORTED; nothing is launched and the output
-    is untouched."""
+    """256 rows of 64K tokens at 32 query heads with an FP32 cache take
+    4096-token work items on the block-size-16 kernel: 16 chunk partials per
+    (row, query head), 68 MB. The call fails on the host with
+    KVFLUX_ERR_UNSUPPORTED; nothing is launched and the output is
+    untouched."""
     lib = capi.lib()
     H, Hq, D, bs = 8, 32, 128, 16
     rows, kv_len = 256, 65536
