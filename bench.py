@@ -22,6 +22,9 @@ Also measured in the same run (sub-objects of the JSON line):
            (device batch table) against the reference API's composition
   offload: GPU <-> CPU chunk transfer (tiered cache), per-chunk DMA against
            one kernel per batch, and overlap with the decode kernel
+  gather_BFloat16.cpu_baseline : the CPU oracle's gather (one thread) on 16
+           of the 64 sequences, pages in a shuffled host cache, in the GPU
+           figure's bytes.
   cpu_baseline : the CPU oracle (gather + double-precision attention, one
            thread) on a bounded sample of the decode rows, timed here; the
            same rows on all cores of the process's CPU share (at most 16) in
@@ -574,9 +577,50 @@ def bench_gather(v2, args, stream, dtype_name: str):
         mism += int((gk != ek).sum() + (gv != ev).sum())
     pages = int(sum((int(L) + bs - 1) // bs for L in lens))
     bytes_step = 8192 * total + 8 * pages
+    out = {"dtype": dtype_name, "kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9,
+           "bytes": bytes_step, "api_us": api_us, "tokens": total, "mismatched_elements_sampled": mism}
+    if dtype_name == "BFloat16":
+        out["cpu_baseline"] = cpu_gather_baseline(kb, vb, mat, lens, H, bs, D, code, rng)
     del seqs
-    return {"dtype": dtype_name, "kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9,
-            "bytes": bytes_step, "api_us": api_us, "tokens": total, "mismatched_elements_sampled": mism}
+    return out
+
+
+def cpu_gather_baseline(kb, vb, mat, lens, H, bs, D, code, rng, sample_rows=16):
+    """The CPU oracle's gather (one thread) on a bounded sample of the
+    gather batch: the sampled sequences' pages copied to a host cache in a
+    shuffled order (so the CPU reads scattered pages too), then every
+    sampled sequence gathered; throughput in the GPU figure's bytes."""
+    from kvflux_amd import device
+    from oracle import oracle
+
+    rows = sorted(rng.choice(len(lens), sample_rows, replace=False).tolist())
+    page_elems = H * bs * D
+    npgs = [(int(lens[r]) + bs - 1) // bs for r in rows]
+    order = rng.permutation(sum(npgs))
+    kc = np.empty(sum(npgs) * page_elems, np.uint16)
+    vc = np.empty_like(kc)
+    tables, slot = [], 0
+    for r, npg in zip(rows, npgs):
+        t = order[slot:slot + npg].astype(np.uint64)
+        for j, dst in enumerate(t.tolist()):
+            src = int(mat[r, j]) * page_elems * 2
+            kc[dst * page_elems:(dst + 1) * page_elems] = device.memcpy_d2h(kb + src, page_elems * 2, np.uint16)
+            vc[dst * page_elems:(dst + 1) * page_elems] = device.memcpy_d2h(vb + src, page_elems * 2, np.uint16)
+        tables.append(t)
+        slot += npg
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 2.0:  # about 2 s of gathering
+        for r, t in zip(rows, tables):
+            oracle.gather_paged_kv(kc, vc, H, bs, D, code, t, int(lens[r]))
+        reps += 1
+    sec = (time.perf_counter() - t0) / reps
+    tokens = int(sum(int(lens[r]) for r in rows))
+    moved = 8192 * tokens + 8 * sum(npgs)
+    return {"value": moved / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port", "seconds": sec,
+            "repetitions": reps,
+            "sample": f"{sample_rows} of the 64 sequences ({tokens} tokens, {moved / 1e9:.3f} GB moved), pages "
+                      "in a shuffled host cache, one thread, averaged over the repetitions"}
 
 
 # --------------------------------------------------------------------- prefill
