@@ -25,6 +25,8 @@ Also measured in the same run (sub-objects of the JSON line):
   gather_BFloat16.cpu_baseline : the CPU oracle's gather (one thread) on 16
            of the 64 sequences, pages in a shuffled host cache, in the GPU
            figure's bytes.
+  prefill.cpu_baseline : the oracle calls that check the prefill's 128
+           sampled rows, timed (8 threads).
   cpu_baseline : the CPU oracle (gather + double-precision attention, one
            thread) on a bounded sample of the decode rows, timed here; the
            same rows on all cores of the process's CPU share (at most 16) in
@@ -684,6 +686,7 @@ def bench_prefill(v2, args, stream):
     page_bytes = H * bs * D * 2
     err = 0.0
     checked = 0
+    cpu_s, cpu_flops = 0.0, 0.0
     local = np.arange(npages, dtype=np.uint64)
     for i in range(S):
         ids = device.memcpy_d2h(tables[i].ptr, npages * 8, np.uint64)
@@ -692,9 +695,12 @@ def bench_prefill(v2, args, stream):
         rows = sorted({0, 63, 64, 1000, 2047, 2048, 4094, 4095} | set(rng.integers(0, T, 8).tolist()))
         qall = device.memcpy_d2h(qs[i].ptr, T * Hq * D * 4, np.float32).reshape(T, Hq * D)
         oall = device.memcpy_d2h(out.ptr + i * T * Hq * D * 4, T * Hq * D * 4, np.float32).reshape(T, Hq * D)
+        t0 = time.perf_counter()
         ref = oracle.paged_attention_rows(kc, vc, H, bs, D, oracle.BF16, np.tile(local, len(rows)), npages,
                                           np.array([t + 1 for t in rows], np.uint64), qall[rows].reshape(-1), Hq,
                                           threads=8)
+        cpu_s += time.perf_counter() - t0
+        cpu_flops += sum(4.0 * Hq * D * (t + 1) for t in rows)
         err = max(err, float(np.abs(oall[rows].reshape(-1) - ref).max()))
         checked += len(rows)
     del seqs
@@ -707,7 +713,13 @@ def bench_prefill(v2, args, stream):
             # 2.05 GHz under this load), so above the FLOP share of the 2.4 GHz
             # spec peak above.
             "mfma_busy_pct": read_prefill_busy(), "mfma_busy_source": "profiles/prefill_counters.txt",
-            "max_abs_err_vs_oracle": err, "rows_checked": checked, "tolerance": 2e-2}
+            "max_abs_err_vs_oracle": err, "rows_checked": checked, "tolerance": 2e-2,
+            # The checked rows' oracle calls, timed: causal attention of each
+            # row in double precision after a page gather, on 8 threads.
+            "cpu_baseline": {"value": cpu_flops / cpu_s / 1e12, "unit": "TFLOP/s", "cores": 8, "kind": "port",
+                             "seconds": cpu_s,
+                             "sample": f"{checked} rows (16 of each sequence, all 32 query heads): page gather + "
+                                       "double-precision causal attention per row"}}
 
 
 def bench_ceilings(v2, args, stream):
