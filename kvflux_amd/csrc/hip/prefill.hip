@@ -249,9 +249,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             pages[i] = ok ? static_cast<std::uint32_t>(id) : kPfMissing;
         }
     };
-    stage(first_page(tile_begin & ~win_mask));
-
-    Vec qb_op[kPfNt][kSteps];
+    // The query rows' loads go out before the page list's, so the two round
+    // trips overlap; the rows are rounded to the cache dtype after.
+    float4 qraw[kPfNt][kSteps][2];
     std::uint32_t row_token[kPfNt];
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
@@ -264,8 +264,17 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             query + (static_cast<std::uint64_t>(tq_safe) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
 #pragma unroll
         for (int kk = 0; kk < kSteps; ++kk) {
-            const float4 lo = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8);
-            const float4 hi = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8 + 4);
+            qraw[n][kk][0] = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8);
+            qraw[n][kk][1] = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8 + 4);
+        }
+    }
+    stage(first_page(tile_begin & ~win_mask));
+    Vec qb_op[kPfNt][kSteps];
+#pragma unroll
+    for (int n = 0; n < kPfNt; ++n) {
+#pragma unroll
+        for (int kk = 0; kk < kSteps; ++kk) {
+            const float4 lo = qraw[n][kk][0], hi = qraw[n][kk][1];
             const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             std::uint32_t w[4];
 #pragma unroll
@@ -364,6 +373,22 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             const std::uint32_t k0 = tile * kPfTile + 32 * h;
             if (k0 > last_key) break;  // uniform
             pf_f32x4_t s[2][kPfNt];
+            // V^T operands of the half-tile (head_size 128): read right after
+            // K, so the LDS reads run under the QK^T MFMAs and the softmax;
+            // P*V takes them from registers (8 x 4096 tokens, 32/8 heads:
+            // 1.267 -> 1.245 ms). At 64 that measured 13% slower, and at 256
+            // they would not fit the registers: there they are read inside P*V.
+            const auto* vbase = (__attribute__((address_space(3))) char*)(
+                (__attribute__((address_space(3))) std::uint16_t*)vt);
+            auto read_v = [&](int dt) {
+                const std::uint32_t off = (v_read0 ^ (dt << 5)) + 32 * h * kRowBytes;
+                const pf_i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off));
+                const pf_i16x4_t hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off + 16 * kRowBytes));
+                return __builtin_bit_cast(Vec, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            };
+            constexpr bool kEarlyV = kD == 128;
+            Vec vop[kEarlyV ? kDt : 1];
             set_priority<1>();
             {
                 Vec a[kSteps][2];
@@ -384,6 +409,14 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                     for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
                         for (int n = 0; n < kPfNt; ++n) s[kt2][n] = M::mma(a[kk][kt2], qb_op[n][kk], s[kt2][n]);
+                if constexpr (kEarlyV) {
+#pragma unroll
+                    for (int dt = 0; dt < kDt; ++dt) vop[dt] = read_v(dt);
+                    // The K reads first, then the MFMAs, then the V reads.
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kSteps, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kSteps * kPfNt, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kDt, 0);
+                }
             }
             set_priority<0>();
             if (k0 + 31 > min_limit) {
@@ -436,15 +469,14 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                 }
                 pb[n] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
             }
-            const auto* vbase = (__attribute__((address_space(3))) char*)(
-                (__attribute__((address_space(3))) std::uint16_t*)vt);
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
-                const std::uint32_t off = (v_read0 ^ (dt << 5)) + 32 * h * kRowBytes;
-                const pf_i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off));
-                const pf_i16x4_t hi =
-                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off + 16 * kRowBytes));
-                const Vec a = __builtin_bit_cast(Vec, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                Vec a;
+                if constexpr (kEarlyV) {
+                    a = vop[dt];
+                } else {
+                    a = read_v(dt);
+                }
 #pragma unroll
                 for (int n = 0; n < kPfNt; ++n) acc[dt][n] = M::mma(a, pb[n], acc[dt][n]);
             }
