@@ -103,8 +103,8 @@ CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("Float16", 1, 3, 256, 32, 300, 120),
     ("BFloat16", 2, 8, 256, 16, 260, 260),
     ("BFloat16", 1, 16, 256, 64, 150, 150),
-    # long prompts; the workgroup's page list holds 8192 pages (4096 at
-    # head_size 256) at a time and is restaged at each window boundary
+    # long prompts; the workgroup's page list holds 2048 pages at a time and
+    # is restaged at each window boundary
     ("BFloat16", 2, 8, 128, 16, 40000, 64),
     ("Float16", 1, 2, 256, 16, 40000, 40),
     ("BFloat16", 1, 4, 64, 4, 30000, 33),
@@ -383,4 +383,74 @@ def test_prefill_batch_matches_single_calls(gpu, name, kv_heads, q_heads, head_s
                                           width, np.array([kv - ql + t + 1 for t in pick], np.uint64),
                                           qi.reshape(ql, row)[pick].reshape(-1), q_heads, threads=8)
         assert np.abs(got[o0:o0 + ql][pick].reshape(-1) - exp).max() < 2e-2
+    assert np.all(got[~used] == 555.0)
+
+
+def random_batch_configs(count, seed):
+    """Seeded draws over the prefill's shape space: dtype, head_size, kv
+    heads, GQA group, page size and a batch of 1-4 sequences, each a whole
+    prompt or a trailing chunk."""
+    rng = np.random.default_rng(seed)
+    configs = []
+    for _ in range(count):
+        name = ("BFloat16", "Float16")[int(rng.integers(2))]
+        head_size = int(rng.choice([64, 128, 256]))
+        kv_heads = int(rng.integers(1, 3))
+        group = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 16]))
+        bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64, 128, 256]))
+        seqs = []
+        for _ in range(int(rng.integers(1, 5))):
+            kv = int(rng.integers(1, 1501))
+            ql = kv if rng.random() < 0.5 else int(rng.integers(1, kv + 1))
+            seqs.append((kv, ql))
+        configs.append((name, kv_heads, kv_heads * group, head_size, bs, seqs))
+    return configs
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_prefill_batch_random_shapes(gpu, case):
+    """kvflux_paged_prefill_batch over seeded random shapes: sampled rows of
+    every sequence (first, last, middle) against the oracle at 2e-2 and
+    against the float64 emulation of the kernel's rounding at 4e-3; rows
+    outside the sequences untouched."""
+    name, kv_heads, q_heads, head_size, bs, seqs = random_batch_configs(10, 4242)[case]
+    lib = capi.lib()
+    n = len(seqs)
+    width = max((kv + bs - 1) // bs for kv, _ in seqs) + 2
+    blocks = n * width + 3
+    kc, vc, _ = setup_case(name, blocks, kv_heads, bs, head_size, 1, 90 + case)
+    order = np.random.default_rng(91 + case).permutation(blocks).astype(np.uint64)
+    table = np.full((n, width), 2**64 - 1, np.uint64)
+    for i, (kv, _) in enumerate(seqs):
+        npg = (kv + bs - 1) // bs
+        table[i, :npg] = order[i * width:i * width + npg]
+    q_lens = np.array([ql for _, ql in seqs], np.uint64)
+    kv_lens = np.array([kv for kv, _ in seqs], np.uint64)
+    offsets = np.concatenate([[0], np.cumsum(q_lens + 1)[:-1]]).astype(np.uint64)
+    rows_total = int(offsets[-1] + q_lens[-1] + 1)
+    row = q_heads * head_size
+    q = oracle.random_elements(0, rows_total * row, oracle.F32, 1, 92 + case)
+    td, qd = buffer_like(table.reshape(-1)), buffer_like(q)
+    kd, ld, od_ = buffer_like(kv_lens), buffer_like(q_lens), buffer_like(offsets)
+    out = buffer_like(np.full(rows_total * row, 555.0, np.float32))
+    assert lib.kvflux_paged_prefill_batch(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, CODES[name], td.ptr,
+                                          width, kd.ptr, ld.ptr, od_.ptr, n, int(q_lens.max()), int(kv_lens.max()),
+                                          q_heads, qd.ptr, out.ptr, None) == 0, capi.last_error()
+    device.synchronize()
+    got = out.download(np.float32).reshape(rows_total, row)
+    used = np.zeros(rows_total, bool)
+    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    for i, (kv, ql) in enumerate(seqs):
+        o0 = int(offsets[i])
+        used[o0:o0 + ql] = True
+        qi = q.reshape(rows_total, row)[o0:o0 + ql].reshape(-1)
+        pick = sorted({0, ql - 1, ql // 2})
+        exp = oracle.paged_attention_rows(kh, vh, kv_heads, bs, head_size, CODES[name], np.tile(table[i], len(pick)),
+                                          width, np.array([kv - ql + t + 1 for t in pick], np.uint64),
+                                          qi.reshape(ql, row)[pick].reshape(-1), q_heads, threads=8)
+        sub = got[o0:o0 + ql][pick]
+        assert np.all(np.isfinite(sub))
+        assert np.abs(sub.reshape(-1) - exp).max() < 2e-2, (i, kv, ql)
+        emu = emulate(kh, vh, name, kv_heads, bs, head_size, table[i], kv, qi, ql, q_heads, pick)
+        assert np.abs(sub.reshape(len(pick), q_heads, head_size) - emu).max() < 4e-3, (i, kv, ql)
     assert np.all(got[~used] == 555.0)
