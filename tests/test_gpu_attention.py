@@ -444,3 +444,66 @@ def test_decode_small_pages_item_sizes(gpu, name, bs, head_size):
     exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table[sample].reshape(-1), width,
                                       lens[sample], q.reshape(rows, -1)[sample].reshape(-1), Hq, threads=8)
     assert np.abs(got[sample].reshape(-1) - exp).max() < TOL
+
+
+def random_decode_configs(count, seed):
+    """Seeded draws over the decode's shape space: cache dtype, head_size
+    (tuned and generic), kv heads, GQA group, page size and a ragged batch
+    whose lengths include page and tile boundaries."""
+    rng = np.random.default_rng(seed)
+    configs = []
+    for _ in range(count):
+        name = ("BFloat16", "Float16", "Float32")[int(rng.integers(3))]
+        head_size = int(rng.choice([64, 80, 128, 256]))
+        H = int(rng.choice([1, 2, 4]))
+        group = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 12, 16]))
+        bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64, 128]))
+        rows = int(rng.integers(1, 13))
+        lens = rng.integers(1, 5001, rows)
+        for r in range(0, rows, 3):  # every third row on a page or tile boundary
+            lens[r] = max(1, int(lens[r]) // max(bs, 16) * max(bs, 16))
+        configs.append((name, head_size, H, H * group, bs, lens.astype(np.uint64)))
+    return configs
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_decode_random_shapes(gpu, case):
+    """kvflux_paged_attention over seeded random shapes (every kernel family
+    the dispatch can pick): the oracle at 1e-5, bit-identical on repeat,
+    nothing written past the output."""
+    name, head_size, H, Hq, bs, lens = random_decode_configs(12, 777)[case]
+    lib = capi.lib()
+    code, host = DTYPES[name]
+    rows = lens.size
+    max_len = int(lens.max())
+    width = (max_len + bs - 1) // bs
+    P = max(64, 2 * width)
+    page = H * bs * head_size
+    kc = device.DeviceBuffer(P * page * np.dtype(host).itemsize)
+    vc = device.DeviceBuffer(P * page * np.dtype(host).itemsize)
+    device.fill_random(kc.ptr, P * page, code, 1, 300 + case)
+    device.fill_random(vc.ptr, P * page, code, 1, 400 + case)
+    rng = np.random.default_rng(500 + case)
+    table = rng.integers(0, P, (rows, width)).astype(np.uint64)
+    for r in range(rows):
+        table[r, (int(lens[r]) + bs - 1) // bs:] = 2**64 - 1
+    td, ld = buffer_like(table.reshape(-1)), buffer_like(lens)
+    q = oracle.random_elements(0, rows * Hq * head_size, oracle.F32, 1, 600 + case)
+    qd = buffer_like(q)
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_attention_workspace_size(rows, max_len, H, Hq, bs, head_size, C.byref(ws)))
+    wd = device.DeviceBuffer(max(ws.value, 256))
+    outs = []
+    for _ in range(2):
+        od = buffer_like(np.full(q.size + 8, 7.0, np.float32))
+        capi.check(lib.kvflux_paged_attention(kc.ptr, vc.ptr, P, H, bs, head_size, code, td.ptr, width, ld.ptr,
+                                              max_len, rows, Hq, qd.ptr, od.ptr, wd.ptr, ws.value, None))
+        device.synchronize()
+        out = od.download(np.float32)
+        assert np.all(out[q.size:] == 7.0)
+        outs.append(out[:q.size])
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    kh, vh = kc.download(host), vc.download(host)
+    exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table.reshape(-1), width, lens, q, Hq,
+                                      threads=8)
+    assert np.abs(outs[0] - exp).max() < TOL
