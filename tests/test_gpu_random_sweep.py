@@ -8,8 +8,11 @@ a batch, then checks
     run), nothing written past the output;
   * batch prefill (kvflux_paged_prefill_batch): sampled rows of every
     sequence (first, middle, last, one random) against the oracle at 2e-2,
-    nothing written past the output.
-KVFLUX_SWEEP_CASES sets the number of cases (default 40: 20 of each);
+    nothing written past the output;
+  * write then gather (kvflux_write_paged_kv, kvflux_gather_paged_kv): random
+    bit patterns, bit-exact against the oracle over the whole arena and the
+    whole outputs.
+KVFLUX_SWEEP_CASES sets the number of cases per test (default 40);
 KVFLUX_SWEEP_SEED the seed (default 777). The oracle's work per case is
 bounded so a case takes well under a second.
 """
@@ -124,7 +127,68 @@ def prefill_case(rng, i):
         assert err < 2e-2, (cfg, k, err)
 
 
+def write_gather_case(rng, i):
+    """A scattered write of random bit patterns (NaN encodings included) into
+    a pre-filled arena, then a ragged gather of random sequences: both
+    bit-exact against the oracle, whole arena and whole outputs compared."""
+    name = ("BFloat16", "Float16", "Float32")[int(rng.integers(3))]
+    code, host = DTYPES[name]
+    H = int(rng.integers(1, 9))
+    D = int(rng.choice([1, 2, 3, 5, 8, 16, 24, 64, 96, 128, 256, 512]))
+    bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64, 128, 256]))
+    page = H * bs * D
+    itemsize = np.dtype(host).itemsize
+    blocks = int(min(rng.integers(1, 200), max(1, 32e6 // (page * itemsize))))  # arenas up to 32 MB
+    bits = np.uint32 if itemsize == 4 else np.uint16
+    arena_k = rng.integers(0, np.iinfo(bits).max, blocks * page, dtype=np.uint64).astype(bits)
+    arena_v = rng.integers(0, np.iinfo(bits).max, blocks * page, dtype=np.uint64).astype(bits)
+    kc, vc = buffer_like(arena_k), buffer_like(arena_v)
+    tokens = int(rng.integers(1, min(blocks * bs, 4096) + 1))
+    slots = rng.choice(blocks * bs, tokens, replace=False).astype(np.uint64)
+    kn = rng.integers(0, np.iinfo(bits).max, tokens * H * D, dtype=np.uint64).astype(bits)
+    vn = rng.integers(0, np.iinfo(bits).max, tokens * H * D, dtype=np.uint64).astype(bits)
+    knd, vnd, sd = buffer_like(kn), buffer_like(vn), buffer_like(slots)
+    lib = capi.lib()
+    capi.check(lib.kvflux_write_paged_kv(kc.ptr, vc.ptr, blocks, H, bs, D, code, knd.ptr, vnd.ptr, sd.ptr, tokens,
+                                         None))
+    device.synchronize()
+    oracle.write_paged_kv(arena_k, arena_v, H, bs, D, code, kn, vn, slots)
+    cfg = f"write {name} H={H} D={D} bs={bs} blocks={blocks} tokens={tokens}"
+    assert np.array_equal(kc.download(bits), arena_k), cfg
+    assert np.array_equal(vc.download(bits), arena_v), cfg
+    # gather: 1-6 sequences over random pages of the written arena
+    n = int(rng.integers(1, 7))
+    lens = rng.integers(1, blocks * bs + 1, n).astype(np.uint64)
+    while int(lens.sum()) * H * D * itemsize > 32e6:  # outputs up to 32 MB
+        lens = (lens // 2 + 1).astype(np.uint64)
+    width = int((lens.max() + bs - 1) // bs)
+    table = rng.integers(0, blocks, (n, width)).astype(np.uint64)
+    offsets = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    total = int(lens.sum())
+    row = H * D
+    ko = buffer_like(np.full(total * row + 8, 0x5A, bits))
+    vo = buffer_like(np.full(total * row + 8, 0x5A, bits))
+    td, ld, od_ = buffer_like(table.reshape(-1)), buffer_like(lens), buffer_like(offsets)
+    capi.check(lib.kvflux_gather_paged_kv(kc.ptr, vc.ptr, blocks, H, bs, D, code, td.ptr, width, ld.ptr, od_.ptr, n,
+                                          int(lens.max()), ko.ptr, vo.ptr, None))
+    device.synchronize()
+    kg, vg = ko.download(bits), vo.download(bits)
+    cfg = f"gather {name} H={H} D={D} bs={bs} lens={lens.tolist()}"
+    assert np.all(kg[total * row:] == 0x5A) and np.all(vg[total * row:] == 0x5A), cfg
+    for k in range(n):
+        o0, L = int(offsets[k]) * row, int(lens[k])
+        ek, ev = oracle.gather_paged_kv(arena_k, arena_v, H, bs, D, code, table[k], L)
+        assert np.array_equal(kg[o0:o0 + L * row], ek.view(bits)), cfg
+        assert np.array_equal(vg[o0:o0 + L * row], ev.view(bits)), cfg
+
+
 def test_random_sweep(gpu):
     rng = np.random.default_rng(SEED)
     for i in range(CASES):
         (decode_case if i % 2 == 0 else prefill_case)(rng, i)
+
+
+def test_random_write_gather(gpu):
+    rng = np.random.default_rng(SEED + 1)
+    for i in range(CASES):
+        write_gather_case(rng, i)
