@@ -14,7 +14,10 @@ namespace kvflux::v2 {
 //   Exact: FP32 Q and FP32 accumulation of every product; matches the
 //          double-precision CPU reference to ~1e-6 for any KV dtype (the
 //          reference's 1e-5 contract). The reference's own signature below
-//          uses it.
+//          uses it. Calls of 16 or more query tokens on a 16-bit cache at
+//          head_size 64 or 128 (block_size a power of two up to 256) run on
+//          the MFMA prefill with Q and the weights split into three 16-bit
+//          parts (exact products); others on the split-K kernel.
 //   Auto:  Exact, except that calls of query_tokens >= 16 on the shapes the
 //          MFMA prefill takes (16-bit KV cache, head_size 64, 128 or 256,
 //          block_size a power of two up to 256) run there: Q and the softmax

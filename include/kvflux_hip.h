@@ -220,6 +220,23 @@ int kvflux_paged_prefill_split(const void* key_cache, const void* value_cache,
                                uint64_t query_heads, const float* query, float* output,
                                void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* kvflux_paged_prefill_exact: kvflux_paged_prefill_split with the reference's
+ * arithmetic contract (1e-5 against a double-precision evaluation,
+ * reference tests/paged_attention_test.cu:128) instead of 2e-2: Q (scale
+ * folded in) and the softmax weights enter the MFMAs as three 16-bit parts
+ * each, so every product is exact in FP32, and the row sums are FP32 sums of
+ * the weights. About three times the MFMA work of kvflux_paged_prefill_split.
+ * Same arguments, workspace and errors, except that head_size must be 64 or
+ * 128 (256: KVFLUX_ERR_UNSUPPORTED). Replaces paged_attention_kernel
+ * (reference src/v2/paged_attention.cu:108-128, 193-246) for the
+ * reference's own paged_attention signature. */
+int kvflux_paged_prefill_exact(const void* key_cache, const void* value_cache,
+                               uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
+                               uint64_t head_size, int dtype, const uint64_t* block_table,
+                               uint64_t num_table_blocks, uint64_t kv_len, uint64_t query_tokens,
+                               uint64_t query_heads, const float* query, float* output,
+                               void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* kvflux_paged_prefill_batch: kvflux_paged_prefill over num_seqs sequences in
  * one launch (a prefill batch). Sequence i: table row i of block_table
  * (device uint64 [num_seqs][max_blocks_per_seq], the reference's

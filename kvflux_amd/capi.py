@@ -63,6 +63,8 @@ SIGNATURES = {
     "kvflux_paged_prefill_workspace_size": (_i32, [_u64, _u64, _u64, _u64, _u64, C.POINTER(_sz)]),
     "kvflux_paged_prefill_split": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _u64,
                                           _u64, _u64, _vp, _vp, _vp, _u64, _vp]),
+    "kvflux_paged_prefill_exact": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _u64,
+                                          _u64, _u64, _vp, _vp, _vp, _u64, _vp]),
     "kvflux_paged_prefill_batch": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _vp, _vp, _vp,
                                           _u64, _u64, _u64, _u64, _vp, _vp, _vp]),
     "kvflux_copy_pages": (_i32, [_vp, _vp, _u64, _u64, _vp, _u64, _vp]),

@@ -44,12 +44,25 @@ typedef __attribute__((ext_vector_type(2))) __bf16 pf_bf16x2_t;
 typedef __attribute__((ext_vector_type(2))) _Float16 pf_f16x2_t;
 
 // pack(a, b): a in the low half, b in the high half, each rounded to nearest
-// even (one v_cvt_pk_{bf16,f16}_f32).
+// even (one v_cvt_pk_{bf16,f16}_f32). split3(a, b): the same pair as three
+// 16-bit parts whose sum is a and b (each part the rounded remainder of the
+// ones before; the differences are exact in FP32), so an MFMA over the three
+// parts against 16-bit cache values forms FP32-exact products.
 struct PfBf16 {
     using Vec = pf_bf16x8_t;
+    static constexpr bool kExact = false;
     static constexpr std::uint32_t kOnes = 0x3f803f80u;  // two 1.0
     __device__ static std::uint32_t pack(float a, float b) {
         return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_bf16x2_t));
+    }
+    __device__ static void split3(float a, float b, std::uint32_t (&w)[3]) {
+        pf_f32x2_t x{a, b};
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const pf_bf16x2_t h = __builtin_convertvector(x, pf_bf16x2_t);
+            w[i] = __builtin_bit_cast(std::uint32_t, h);
+            x -= __builtin_convertvector(h, pf_f32x2_t);
+        }
     }
     __device__ static pf_f32x4_t mma(const Vec& a, const Vec& b, const pf_f32x4_t& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -57,18 +70,45 @@ struct PfBf16 {
 };
 struct PfF16 {
     using Vec = pf_f16x8_t;
+    static constexpr bool kExact = false;
     static constexpr std::uint32_t kOnes = 0x3c003c00u;  // two 1.0
     __device__ static std::uint32_t pack(float a, float b) {
         return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_f16x2_t));
+    }
+    __device__ static void split3(float a, float b, std::uint32_t (&w)[3]) {
+        pf_f32x2_t x{a, b};
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const pf_f16x2_t h = __builtin_convertvector(x, pf_f16x2_t);
+            w[i] = __builtin_bit_cast(std::uint32_t, h);
+            x -= __builtin_convertvector(h, pf_f32x2_t);
+        }
     }
     __device__ static pf_f32x4_t mma(const Vec& a, const Vec& b, const pf_f32x4_t& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
 };
+// The exact variants: Q and the softmax weights enter the MFMAs as three
+// 16-bit parts each (FP32-exact products, FP32 accumulation), the row sums
+// are FP32 sums of the weights, and a wavefront holds one row block.
+struct PfBf16Exact : PfBf16 {
+    static constexpr bool kExact = true;
+};
+struct PfF16Exact : PfF16 {
+    static constexpr bool kExact = true;
+};
 
 // NaN-propagating maximum of three (one v_maximum3_f32).
 __device__ inline float max3(float a, float b, float c) {
     return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+// Sum over the four lanes l, l^16, l^32, l^48, the same in all four (each
+// level adds a pair in either order).
+__device__ inline float sum_across_quads(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 // Maximum over the four lanes l, l^16, l^32, l^48 (the four quads of a
 // column) with two cross-row lane swaps, no LDS round trip.
@@ -85,6 +125,10 @@ constexpr int kPfWaves = kPfThreads / 64;
 // accumulators and Q operands take as many registers as two blocks at 128).
 template <int kD>
 constexpr int pf_blocks_per_wave() { return kD == 256 ? 1 : 2; }
+// The same for an element policy: one block in the exact variants (their Q
+// operands take three times the registers).
+template <typename E, int kD>
+constexpr int pf_blocks() { return E::kExact ? 1 : pf_blocks_per_wave<kD>(); }
 constexpr int kPfTileShift = 6;
 constexpr int kPfTile = 1 << kPfTileShift;  // keys per LDS tile
 // Page ids held in LDS per workgroup, one window of the sequence at a time:
@@ -180,7 +224,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     constexpr int kRowBytes = kD * 2;
     constexpr int kTileBytes = kPfTile * kRowBytes;
     constexpr int kDma = kTileBytes / (kPfThreads * 16);  // tile loads per thread per cache
-    constexpr int kPfNt = pf_blocks_per_wave<kD>();
+    constexpr int kPfNt = pf_blocks<E, kD>();
+    constexpr bool kExact = E::kExact;
+    constexpr int kParts = kExact ? 3 : 1;  // 16-bit parts of Q and of the weights
     constexpr int kBlocks = kPfWaves * kPfNt;   // 16-row blocks per workgroup
     constexpr int kTok = 16 * (kBlocks / kG);  // query tokens per workgroup
     constexpr int kVSwz = kCpr / 8;            // V slot swizzle multiplier
@@ -269,17 +315,27 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         }
     }
     stage(first_page(tile_begin & ~win_mask));
-    Vec qb_op[kPfNt][kSteps];
+    Vec qb_op[kParts][kPfNt][kSteps];
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
 #pragma unroll
         for (int kk = 0; kk < kSteps; ++kk) {
             const float4 lo = qraw[n][kk][0], hi = qraw[n][kk][1];
             const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            std::uint32_t w[4];
+            std::uint32_t w[kParts][4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = M::pack(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2);
-            qb_op[n][kk] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (kExact) {
+                    std::uint32_t parts[3];
+                    M::split3(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2, parts);
+#pragma unroll
+                    for (int k = 0; k < kParts; ++k) w[k][e] = parts[k];
+                } else {
+                    w[0][e] = M::pack(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kParts; ++k) qb_op[k][n][kk] = __builtin_bit_cast(Vec, make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]));
         }
     }
     __syncthreads();  // pages[] ready (the query loads are complete as well)
@@ -354,6 +410,10 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
         for (int n = 0; n < kPfNt; ++n) acc[dt][n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // Row sums: the MFMA of the rounded weights against ones (the sum the
+    // numerator uses), or in the exact variants each lane's FP32 sum of its
+    // own weights of the row in lane 0 of the vector (added over the four
+    // quads at the end).
     pf_f32x4_t lsum[kPfNt];
     // Minus the row's reference point, in all four accumulator lanes (the
     // seed of every QK^T chain; equal in the four quads of a column).
@@ -408,7 +468,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 #pragma unroll
                     for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
-                        for (int n = 0; n < kPfNt; ++n) s[kt2][n] = M::mma(a[kk][kt2], qb_op[n][kk], s[kt2][n]);
+                        for (int n = 0; n < kPfNt; ++n)
+#pragma unroll
+                            for (int k = 0; k < kParts; ++k) s[kt2][n] = M::mma(a[kk][kt2], qb_op[k][n][kk], s[kt2][n]);
                 if constexpr (kEarlyV) {
 #pragma unroll
                     for (int dt = 0; dt < kDt; ++dt) vop[dt] = read_v(dt);
@@ -458,16 +520,30 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                 }
                 have_ref = true;
             }
-            Vec pb[kPfNt];
+            Vec pb[kParts][kPfNt];
 #pragma unroll
             for (int n = 0; n < kPfNt; ++n) {
-                std::uint32_t w[4];
+                float pr[8];
 #pragma unroll
-                for (int kt2 = 0; kt2 < 2; ++kt2) {
-                    w[2 * kt2] = M::pack(__builtin_amdgcn_exp2f(s[kt2][n][0]), __builtin_amdgcn_exp2f(s[kt2][n][1]));
-                    w[2 * kt2 + 1] = M::pack(__builtin_amdgcn_exp2f(s[kt2][n][2]), __builtin_amdgcn_exp2f(s[kt2][n][3]));
+                for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) pr[4 * kt2 + r] = __builtin_amdgcn_exp2f(s[kt2][n][r]);
+                std::uint32_t w[kParts][4];
+                if constexpr (kExact) {
+                    lsum[n][0] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        std::uint32_t parts[3];
+                        M::split3(pr[2 * j], pr[2 * j + 1], parts);
+#pragma unroll
+                        for (int k = 0; k < kParts; ++k) w[k][j] = parts[k];
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) w[0][j] = M::pack(pr[2 * j], pr[2 * j + 1]);
                 }
-                pb[n] = __builtin_bit_cast(Vec, make_uint4(w[0], w[1], w[2], w[3]));
+#pragma unroll
+                for (int k = 0; k < kParts; ++k) pb[k][n] = __builtin_bit_cast(Vec, make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]));
             }
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
@@ -478,10 +554,14 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                     a = read_v(dt);
                 }
 #pragma unroll
-                for (int n = 0; n < kPfNt; ++n) acc[dt][n] = M::mma(a, pb[n], acc[dt][n]);
-            }
+                for (int n = 0; n < kPfNt; ++n)
 #pragma unroll
-            for (int n = 0; n < kPfNt; ++n) lsum[n] = M::mma(ones, pb[n], lsum[n]);
+                    for (int k = 0; k < kParts; ++k) acc[dt][n] = M::mma(a, pb[k][n], acc[dt][n]);
+            }
+            if constexpr (!kExact) {
+#pragma unroll
+                for (int n = 0; n < kPfNt; ++n) lsum[n] = M::mma(ones, pb[0][n], lsum[n]);
+            }
         }
     };
 
@@ -536,7 +616,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
-        const float l = lsum[n][0];
+        const float l = kExact ? sum_across_quads(lsum[n][0]) : lsum[n][0];
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const int b = wave * kPfNt + n;
         const int g = b % kG;
@@ -601,7 +681,7 @@ __global__ __launch_bounds__(256) void paged_prefill_combine_kernel(const float*
 template <typename E, int kD, int kG>
 int launch_prefill_pass(const PrefillParams& p, hipStream_t s) {
     PrefillParams q = p;
-    constexpr unsigned kTok = 16 * (kPfWaves * pf_blocks_per_wave<kD>() / kG);
+    constexpr unsigned kTok = 16 * (kPfWaves * pf_blocks<E, kD>() / kG);
     // tq: the query tokens of the sequence, or the most of any sequence of a batch.
     q.qblocks = (p.tq + kTok - 1) / kTok;
     const std::uint64_t grid = static_cast<std::uint64_t>(q.qblocks) * p.heads * (p.num_seqs ? p.num_seqs : p.splits);
@@ -625,7 +705,7 @@ inline std::uint32_t prefill_sub_group(std::uint32_t group, std::uint32_t blocks
 
 template <typename E, int kD>
 int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_t s) {
-    constexpr int kBlocks = kPfWaves * pf_blocks_per_wave<kD>();
+    constexpr int kBlocks = kPfWaves * pf_blocks<E, kD>();
     const std::uint32_t sub = prefill_sub_group(group, kBlocks);
     PrefillParams q = p;
     q.q_group = group;
@@ -665,7 +745,13 @@ int launch_prefill_head_size(const PrefillParams& p, std::uint64_t head_size, st
     switch (head_size) {
     case 64: return launch_prefill_group<E, 64>(p, group, s);
     case 128: return launch_prefill_group<E, 128>(p, group, s);
-    default: return launch_prefill_group<E, 256>(p, group, s);
+    default:
+        if constexpr (E::kExact) {
+            return fail(KVFLUX_ERR_UNSUPPORTED, "exact paged prefill: head_size %llu",
+                        static_cast<unsigned long long>(head_size));
+        } else {
+            return launch_prefill_group<E, 256>(p, group, s);
+        }
     }
 }
 
@@ -681,8 +767,9 @@ struct PrefillPlan {
 // most 32. Partials: [splits][tq][query_heads] rows of D floats, then the
 // same rows of {reference point, weight sum}.
 inline PrefillPlan prefill_plan(std::uint64_t head_size, std::uint64_t group, std::uint64_t num_kv_heads,
-                                std::uint64_t kv_len, std::uint64_t query_tokens, std::uint64_t query_heads) {
-    const std::uint64_t blocks = head_size == 256 ? kPfWaves : 2 * kPfWaves;
+                                std::uint64_t kv_len, std::uint64_t query_tokens, std::uint64_t query_heads,
+                                bool exact = false) {
+    const std::uint64_t blocks = head_size == 256 || exact ? kPfWaves : 2 * kPfWaves;
     const std::uint64_t sub = prefill_sub_group(static_cast<std::uint32_t>(group), static_cast<std::uint32_t>(blocks));
     const std::uint64_t tok = 16 * (blocks / sub);
     const std::uint64_t wgs = (query_tokens + tok - 1) / tok * num_kv_heads;
@@ -707,7 +794,8 @@ namespace {
 int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_blocks, uint64_t num_kv_heads,
                   uint64_t block_size, uint64_t head_size, int dtype, const uint64_t* block_table,
                   uint64_t num_table_blocks, uint64_t kv_len, uint64_t query_tokens, uint64_t query_heads,
-                  const float* query, float* output, void* workspace, uint64_t workspace_bytes, void* stream) {
+                  const float* query, float* output, void* workspace, uint64_t workspace_bytes, void* stream,
+                  bool exact = false) {
     if (query_tokens == 0) return KVFLUX_OK;
     if (dtype_bytes(dtype) == 0) return fail(KVFLUX_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
     if (!key_cache || !value_cache || !block_table || !query || !output) {
@@ -727,6 +815,7 @@ int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_b
         query_heads > 0xffffffffULL || num_kv_heads * block_size * head_size * 2 > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
     }
+    if (exact && head_size == 256) return fail(KVFLUX_ERR_UNSUPPORTED, "exact paged prefill: head_size 256");
 
     PrefillParams p{};
     p.key_cache = key_cache;
@@ -747,7 +836,7 @@ int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_b
     p.splits = 1;
     p.split_tiles = static_cast<std::uint32_t>((kv_len + kPfTile - 1) / kPfTile);
     if (workspace) {
-        const PrefillPlan plan = prefill_plan(head_size, group, num_kv_heads, kv_len, query_tokens, query_heads);
+        const PrefillPlan plan = prefill_plan(head_size, group, num_kv_heads, kv_len, query_tokens, query_heads, exact);
         if (plan.splits > 1) {
             if (workspace_bytes < plan.workspace) {
                 return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill: workspace of %llu bytes, %llu needed",
@@ -762,6 +851,10 @@ int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_b
     }
     const hipStream_t s = as_stream(stream);
     const std::uint32_t g = static_cast<std::uint32_t>(group);
+    if (exact) {
+        if (dtype == KVFLUX_DTYPE_BF16) return launch_prefill_head_size<PfBf16Exact>(p, head_size, g, s);
+        return launch_prefill_head_size<PfF16Exact>(p, head_size, g, s);
+    }
     if (dtype == KVFLUX_DTYPE_BF16) return launch_prefill_head_size<PfBf16>(p, head_size, g, s);
     return launch_prefill_head_size<PfF16>(p, head_size, g, s);
 }
@@ -799,6 +892,16 @@ extern "C" int kvflux_paged_prefill_split(const void* key_cache, const void* val
     return paged_prefill(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype, block_table,
                          num_table_blocks, kv_len, query_tokens, query_heads, query, output, workspace,
                          workspace_bytes, stream);
+}
+
+extern "C" int kvflux_paged_prefill_exact(const void* key_cache, const void* value_cache, uint64_t num_blocks,
+                                          uint64_t num_kv_heads, uint64_t block_size, uint64_t head_size, int dtype,
+                                          const uint64_t* block_table, uint64_t num_table_blocks, uint64_t kv_len,
+                                          uint64_t query_tokens, uint64_t query_heads, const float* query,
+                                          float* output, void* workspace, uint64_t workspace_bytes, void* stream) {
+    return paged_prefill(key_cache, value_cache, num_blocks, num_kv_heads, block_size, head_size, dtype, block_table,
+                         num_table_blocks, kv_len, query_tokens, query_heads, query, output, workspace,
+                         workspace_bytes, stream, true);
 }
 
 extern "C" int kvflux_paged_prefill_batch(const void* key_cache, const void* value_cache, uint64_t num_blocks,

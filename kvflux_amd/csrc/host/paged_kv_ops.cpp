@@ -176,19 +176,33 @@ void read_paged_kv_batch(const PagedKVStorage& storage,
 
 namespace {
 
-// Whether the MFMA prefill takes the call: the precision allows it and the
-// shape is inside the kernel's limits (the same limits kvflux_paged_prefill
-// checks), so its workspace is reserved only for calls that will use it.
-bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len,
-                      AttentionPrecision precision) {
-    if (precision == AttentionPrecision::Exact) return false;
-    if (precision == AttentionPrecision::Auto && query_tokens < 16) return false;
+// Whether a call's shape is inside the MFMA prefill's limits (the same limits
+// kvflux_paged_prefill checks), so its workspace is reserved only for calls
+// that will use it.
+bool prefill_shape_ok(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len) {
     if (query_tokens == 0 || layout.dtype() == DType::Float32) return false;
     if (layout.head_size() != 64 && layout.head_size() != 128 && layout.head_size() != 256) return false;
     const std::size_t bs = layout.block_size();
     if (bs > 256 || (bs & (bs - 1)) != 0) return false;  // a power of two up to 256
     return layout.num_blocks() <= 0x7fffffffULL && layout.num_kv_heads() <= 65535 && kv_len <= 0x7fffffffULL &&
            layout.page_bytes() <= 0xffffffffULL;
+}
+
+// The rounded (2e-2) MFMA prefill: Fast, or Auto from 16 query tokens on.
+bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len,
+                      AttentionPrecision precision) {
+    if (precision == AttentionPrecision::Exact) return false;
+    if (precision == AttentionPrecision::Auto && query_tokens < 16) return false;
+    return prefill_shape_ok(layout, query_tokens, kv_len);
+}
+
+// The exact (1e-5) MFMA prefill: Exact calls of 16 or more query tokens at
+// head_size 64 or 128 (fewer tokens run faster on the split-K kernel).
+bool exact_prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len,
+                            AttentionPrecision precision) {
+    if (precision != AttentionPrecision::Exact || query_tokens < 16) return false;
+    if (layout.head_size() == 256) return false;
+    return prefill_shape_ok(layout, query_tokens, kv_len);
 }
 
 } // namespace
@@ -230,10 +244,12 @@ void paged_attention(const PagedKVStorage& storage, const SequenceState& sequenc
     validate_q_o(storage, query_device, output_device, tensor_bytes);
     const auto dev = storage.scratch().upload({{table.data(), table_bytes}});
     bool launched = false;
-    if (prefill_eligible(layout, query_tokens, sequence.num_tokens(), precision)) {
+    const bool exact_mfma = exact_prefill_eligible(layout, query_tokens, sequence.num_tokens(), precision);
+    if (exact_mfma || prefill_eligible(layout, query_tokens, sequence.num_tokens(), precision)) {
         std::size_t ws_bytes = 0;
         void* ws = prefill_workspace(storage, query_tokens, sequence.num_tokens(), query_heads, &ws_bytes);
-        const int status = kvflux_paged_prefill_split(
+        const auto launch = exact_mfma ? kvflux_paged_prefill_exact : kvflux_paged_prefill_split;
+        const int status = launch(
             storage.key_base(), storage.value_base(), layout.num_blocks(), layout.num_kv_heads(),
             layout.block_size(), layout.head_size(), abi_dtype(layout.dtype()), dev[0],
             table.size(), sequence.num_tokens(), query_tokens, query_heads, query_device,

@@ -130,7 +130,9 @@ def test_shared_prefix_rows(gpu, v2):
 
 
 @pytest.mark.parametrize("name,q_tokens", [("BFloat16", 1), ("BFloat16", 9), ("BFloat16", 37),
-                                           ("Float32", 1), ("Float32", 37), ("Float16", 9)])
+                                           ("Float32", 1), ("Float32", 37), ("Float16", 9),
+                                           # 16 or more tokens on a 16-bit cache: the exact MFMA prefill
+                                           ("Float16", 40), ("BFloat16", 700), ("Float16", 700)])
 def test_causal_trailing_queries_exact(gpu, v2, name, q_tokens):
     pool, storage, seqs, _ = build_batch(v2, name, 2, 128, [700], 80, 11)
     seq = seqs[0]

@@ -454,3 +454,56 @@ def test_prefill_batch_random_shapes(gpu, case):
         emu = emulate(kh, vh, name, kv_heads, bs, head_size, table[i], kv, qi, ql, q_heads, pick)
         assert np.abs(sub.reshape(len(pick), q_heads, head_size) - emu).max() < 4e-3, (i, kv, ql)
     assert np.all(got[~used] == 555.0)
+
+
+EXACT_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
+    ("BFloat16", 2, 8, 128, 16, 1000, 1000),
+    ("Float16", 2, 8, 128, 16, 700, 37),
+    ("BFloat16", 1, 8, 128, 32, 333, 333),
+    ("Float16", 2, 4, 64, 16, 600, 600),
+    ("BFloat16", 2, 6, 128, 16, 500, 500),      # group 6 (two idle blocks of eight)
+    ("BFloat16", 2, 32, 128, 16, 260, 260),     # group 16 as 2 x 8
+    ("Float16", 1, 12, 64, 64, 333, 333),       # group 12 as 2 x 6
+    ("BFloat16", 1, 4, 64, 1, 3000, 300),       # one-token pages
+    ("BFloat16", 2, 8, 128, 128, 1000, 1000),   # pages longer than a tile
+    ("BFloat16", 8, 32, 128, 16, 8192, 64),     # chunked prefill: keys split over workgroups
+    ("Float16", 1, 4, 128, 16, 40000, 16),      # page-list windows, split keys
+]
+
+
+@pytest.mark.parametrize("name,kv_heads,q_heads,head_size,bs,kv_len,q_tokens", EXACT_CASES)
+def test_prefill_exact_matches_reference(gpu, name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens):
+    """kvflux_paged_prefill_exact: Q and the weights in three 16-bit parts,
+    FP32 row sums; the reference's 1e-5 bound against the oracle (whole
+    output), with and without key splits, bit-identical on repeat; head_size
+    256 is declined."""
+    blocks = (kv_len + bs - 1) // bs + 17
+    seed = kv_len + 5 * q_tokens
+    kc, vc, table = setup_case(name, blocks, kv_heads, bs, head_size, kv_len, seed)
+    q = oracle.random_elements(0, q_tokens * q_heads * head_size, oracle.F32, 1, seed)
+    lib = capi.lib()
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_prefill_workspace_size(kv_heads, head_size, kv_len, q_tokens, q_heads, C.byref(ws)))
+    td, qd = buffer_like(table), buffer_like(q)
+    wd = device.DeviceBuffer(max(ws.value, 256))
+    outs = []
+    for workspace in (True, False, True):
+        od = buffer_like(np.full(q.size + 4, 777.0, np.float32))
+        assert lib.kvflux_paged_prefill_exact(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, CODES[name], td.ptr,
+                                              len(table), kv_len, q_tokens, q_heads, qd.ptr, od.ptr,
+                                              wd.ptr if workspace else None, ws.value if workspace else 0,
+                                              None) == 0, capi.last_error()
+        device.synchronize()
+        out = od.download(np.float32)
+        assert np.all(out[q.size:] == 777.0)
+        outs.append(out[:q.size])
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    exp = oracle.paged_attention_causal(kh, vh, kv_heads, bs, head_size, CODES[name], table, kv_len, q, q_tokens,
+                                        q_heads, threads=8)
+    for got in outs[:2]:
+        assert np.all(np.isfinite(got))
+        assert np.abs(got - exp).max() < 1e-5
+    assert lib.kvflux_paged_prefill_exact(kc.ptr, vc.ptr, blocks, kv_heads, bs, 256, CODES[name], td.ptr, len(table),
+                                          kv_len, q_tokens, q_heads, qd.ptr, qd.ptr, None, 0,
+                                          None) == capi.ERR_UNSUPPORTED
