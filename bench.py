@@ -673,7 +673,18 @@ def bench_prefill(v2, args, stream):
             capi.check(lib.kvflux_paged_prefill(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16, tables[i].ptr,
                                                 npages, T, T, Hq, qs[i].ptr, out.ptr + i * T * Hq * D * 4, stream))
 
+    # The reference's arithmetic contract (1e-5): the exact variant, one
+    # launch per sequence, into its own output.
+    out_exact = device.DeviceBuffer(S * T * Hq * D * 4)
+
+    def per_sequence_exact():
+        for i in range(S):
+            capi.check(lib.kvflux_paged_prefill_exact(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16,
+                                                      tables[i].ptr, npages, T, T, Hq, qs[i].ptr,
+                                                      out_exact.ptr + i * T * Hq * D * 4, None, 0, stream))
+
     per_seq_ms = time_launches(per_sequence, stream, max(1, args.warmup // 2), max(3, args.steps // 4))
+    exact_ms = time_launches(per_sequence_exact, stream, 1, max(3, args.steps // 4))
     ms = time_launches(launch, stream, max(1, args.warmup // 2), max(3, args.steps // 4))
     # The synchronous C++ API (paged_attention with AttentionPrecision::Fast,
     # one call per sequence) on the same inputs.
@@ -685,6 +696,7 @@ def bench_prefill(v2, args, stream):
     # boundaries, a seeded sample) against the CPU reference.
     page_bytes = H * bs * D * 2
     err = 0.0
+    err_exact = 0.0
     checked = 0
     cpu_s, cpu_flops = 0.0, 0.0
     local = np.arange(npages, dtype=np.uint64)
@@ -702,6 +714,8 @@ def bench_prefill(v2, args, stream):
         cpu_s += time.perf_counter() - t0
         cpu_flops += sum(4.0 * Hq * D * (t + 1) for t in rows)
         err = max(err, float(np.abs(oall[rows].reshape(-1) - ref).max()))
+        oex = device.memcpy_d2h(out_exact.ptr + i * T * Hq * D * 4, T * Hq * D * 4, np.float32).reshape(T, Hq * D)
+        err_exact = max(err_exact, float(np.abs(oex[rows].reshape(-1) - ref).max()))
         checked += len(rows)
     del seqs
     tflops = flops / (ms * 1e-3) / 1e12
@@ -714,6 +728,11 @@ def bench_prefill(v2, args, stream):
             # spec peak above.
             "mfma_busy_pct": read_prefill_busy(), "mfma_busy_source": "profiles/prefill_counters.txt",
             "max_abs_err_vs_oracle": err, "rows_checked": checked, "tolerance": 2e-2,
+            # The exact variant (kvflux_paged_prefill_exact: Q and weights as
+            # three 16-bit parts), one launch per sequence, at the
+            # reference's 1e-5 bound on the same checked rows.
+            "exact": {"ms": exact_ms, "TFLOPs": flops / (exact_ms * 1e-3) / 1e12,
+                      "max_abs_err_vs_oracle": err_exact, "tolerance": 1e-5},
             # The checked rows' oracle calls, timed: causal attention of each
             # row in double precision after a page gather, on 8 threads.
             "cpu_baseline": {"value": cpu_flops / cpu_s / 1e12, "unit": "TFLOP/s", "cores": 8, "kind": "port",
