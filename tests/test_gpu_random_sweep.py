@@ -11,7 +11,9 @@ a batch, then checks
     nothing written past the output;
   * write then gather (kvflux_write_paged_kv, kvflux_gather_paged_kv): random
     bit patterns, bit-exact against the oracle over the whole arena and the
-    whole outputs.
+    whole outputs;
+  * the exact prefill (kvflux_paged_prefill_exact): every output of one
+    sequence against the oracle at 1e-5 (a quarter as many cases).
 KVFLUX_SWEEP_CASES sets the number of cases per test (default 40);
 KVFLUX_SWEEP_SEED the seed (default 777). The oracle's work per case is
 bounded so a case takes well under a second.
@@ -180,6 +182,52 @@ def write_gather_case(rng, i):
         ek, ev = oracle.gather_paged_kv(arena_k, arena_v, H, bs, D, code, table[k], L)
         assert np.array_equal(kg[o0:o0 + L * row], ek.view(bits)), cfg
         assert np.array_equal(vg[o0:o0 + L * row], ev.view(bits)), cfg
+
+
+def exact_prefill_case(rng, i):
+    """kvflux_paged_prefill_exact on one sequence (a whole prompt or a
+    trailing chunk, with its workspace so keys may split): every output
+    against the oracle at 1e-5."""
+    name = ("BFloat16", "Float16")[int(rng.integers(2))]
+    D = int(rng.choice([64, 128]))
+    H = int(rng.choice([1, 2, 4]))
+    Hq = H * int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 16]))
+    bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64, 128, 256]))
+    kv = int(rng.integers(16, int(rng.choice([300, 3000, 12000])) + 1))
+    ql = kv if rng.random() < 0.5 else int(rng.integers(16, kv + 1))
+    while ql * kv * Hq * D > 2e9:  # bound the oracle's work
+        ql = max(16, ql // 2)
+    code = DTYPES[name][0]
+    npg = (kv + bs - 1) // bs
+    blocks = npg + 5
+    page = H * bs * D
+    kc, vc = device.DeviceBuffer(blocks * page * 2), device.DeviceBuffer(blocks * page * 2)
+    device.fill_random(kc.ptr, blocks * page, code, 1, 7000 + i)
+    device.fill_random(vc.ptr, blocks * page, code, 1, 8000 + i)
+    table = rng.permutation(blocks)[:npg].astype(np.uint64)
+    q = oracle.random_elements(0, ql * Hq * D, oracle.F32, 1, 9000 + i)
+    lib = capi.lib()
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_prefill_workspace_size(H, D, kv, ql, Hq, C.byref(ws)))
+    wd = device.DeviceBuffer(max(ws.value, 256))
+    td, qd = buffer_like(table), buffer_like(q)
+    od = buffer_like(np.full(q.size + 8, 555.0, np.float32))
+    capi.check(lib.kvflux_paged_prefill_exact(kc.ptr, vc.ptr, blocks, H, bs, D, code, td.ptr, npg, kv, ql, Hq, qd.ptr,
+                                              od.ptr, wd.ptr, ws.value, None))
+    device.synchronize()
+    out = od.download(np.float32)
+    cfg = f"exact prefill {name} D={D} H={H} Hq={Hq} bs={bs} kv={kv} q={ql}"
+    assert np.all(out[q.size:] == 555.0), cfg
+    exp = oracle.paged_attention_causal(kc.download(np.uint16), vc.download(np.uint16), H, bs, D, code, table, kv, q,
+                                        ql, Hq, threads=8)
+    err = float(np.abs(out[:q.size] - exp).max())
+    assert err < 1e-5, (cfg, err)
+
+
+def test_random_exact_prefill(gpu):
+    rng = np.random.default_rng(SEED + 2)
+    for i in range(max(1, CASES // 4)):
+        exact_prefill_case(rng, i)
 
 
 def test_random_sweep(gpu):
