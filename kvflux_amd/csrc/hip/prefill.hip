@@ -476,7 +476,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                     for (int dt = 0; dt < kDt; ++dt) vop[dt] = read_v(dt);
                     // The K reads first, then the MFMAs, then the V reads.
                     __builtin_amdgcn_sched_group_barrier(0x100, 2 * kSteps, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kSteps * kPfNt, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kSteps * kPfNt * kParts, 0);
                     __builtin_amdgcn_sched_group_barrier(0x100, 2 * kDt, 0);
                 }
             }
