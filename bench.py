@@ -61,6 +61,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
+PEAK_FP32_MFMA_TFLOPS = 157.3  # dense FP32 MFMA
 TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_bs16_traffic.txt"
 PREFILL_COUNTERS = ROOT / "profiles" / "prefill_counters.txt"
 METRIC = "decode paged-attn HBM TB/s (% of peak) + KV write/gather GB/s, 1 GPU"
@@ -683,8 +684,21 @@ def bench_prefill(v2, args, stream):
                                                       tables[i].ptr, npages, T, T, Hq, qs[i].ptr,
                                                       out_exact.ptr + i * T * Hq * D * 4, None, 0, stream))
 
+    # FP32 caches holding the same values (BF16 widened exactly), one batch
+    # launch on FP32 MFMAs; the same oracle rows apply.
+    cache_bytes = storage.layout().cache_bytes()
+    k32 = device.to_device((device.memcpy_d2h(kb, cache_bytes, np.uint16).astype(np.uint32) << 16).view(np.float32))
+    v32 = device.to_device((device.memcpy_d2h(vb, cache_bytes, np.uint16).astype(np.uint32) << 16).view(np.float32))
+    out_f32 = device.DeviceBuffer(S * T * Hq * D * 4)
+
+    def launch_f32():
+        capi.check(lib.kvflux_paged_prefill_batch(k32.ptr, v32.ptr, pool.capacity(), H, bs, D, capi.DTYPE_F32,
+                                                  batch_table.ptr, npages, kv_lens.ptr, kv_lens.ptr, q_offs.ptr, S, T,
+                                                  T, Hq, q_all.ptr, out_f32.ptr, stream))
+
     per_seq_ms = time_launches(per_sequence, stream, max(1, args.warmup // 2), max(3, args.steps // 4))
     exact_ms = time_launches(per_sequence_exact, stream, 1, max(3, args.steps // 4))
+    f32_ms = time_launches(launch_f32, stream, 1, max(3, args.steps // 4))
     ms = time_launches(launch, stream, max(1, args.warmup // 2), max(3, args.steps // 4))
     # The synchronous C++ API (paged_attention with AttentionPrecision::Fast,
     # one call per sequence) on the same inputs.
@@ -697,6 +711,7 @@ def bench_prefill(v2, args, stream):
     page_bytes = H * bs * D * 2
     err = 0.0
     err_exact = 0.0
+    err_f32 = 0.0
     checked = 0
     cpu_s, cpu_flops = 0.0, 0.0
     local = np.arange(npages, dtype=np.uint64)
@@ -716,6 +731,8 @@ def bench_prefill(v2, args, stream):
         err = max(err, float(np.abs(oall[rows].reshape(-1) - ref).max()))
         oex = device.memcpy_d2h(out_exact.ptr + i * T * Hq * D * 4, T * Hq * D * 4, np.float32).reshape(T, Hq * D)
         err_exact = max(err_exact, float(np.abs(oex[rows].reshape(-1) - ref).max()))
+        of32 = device.memcpy_d2h(out_f32.ptr + i * T * Hq * D * 4, T * Hq * D * 4, np.float32).reshape(T, Hq * D)
+        err_f32 = max(err_f32, float(np.abs(of32[rows].reshape(-1) - ref).max()))
         checked += len(rows)
     del seqs
     tflops = flops / (ms * 1e-3) / 1e12
@@ -733,6 +750,12 @@ def bench_prefill(v2, args, stream):
             # reference's 1e-5 bound on the same checked rows.
             "exact": {"ms": exact_ms, "TFLOPs": flops / (exact_ms * 1e-3) / 1e12,
                       "max_abs_err_vs_oracle": err_exact, "tolerance": 1e-5},
+            # FP32 caches (the same values): one batch launch on
+            # v_mfma_f32_16x16x4_f32, against the FP32 MFMA peak.
+            "f32": {"kernel": "paged_prefill_kernel<f32,128,4>, one batch launch", "ms": f32_ms,
+                    "TFLOPs": flops / (f32_ms * 1e-3) / 1e12,
+                    "frac_of_fp32_mfma_peak": flops / (f32_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+                    "max_abs_err_vs_oracle": err_f32, "tolerance": 1e-5},
             # The checked rows' oracle calls, timed: causal attention of each
             # row in double precision after a page gather, on 8 threads.
             "cpu_baseline": {"value": cpu_flops / cpu_s / 1e12, "unit": "TFLOP/s", "cores": 8, "kind": "port",

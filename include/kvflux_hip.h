@@ -181,15 +181,17 @@ int kvflux_paged_attention_noalloc(const void* key_cache, const void* value_cach
                                    const float* query, float* output, void* stream);
 
 /* ---------------------------------------------------------------------------
- * Hot path 3b: causal paged prefill on MFMA (BF16/FP16 caches only).
+ * Hot path 3b: causal paged prefill on MFMA.
  * Replaces paged_attention_kernel for a whole-prompt call
  * (reference src/v2/paged_attention.cu:108-128, 193-246, query_tokens = Tq).
  * One sequence: block_table device uint64 [ceil(kv_len / block_size)],
  * query i attends to tokens [0, kv_len - query_tokens + i].
- * Q is rounded to the cache dtype and the softmax weights to the cache dtype
- * before the MFMA products; accumulation and softmax are FP32.
- * KVFLUX_ERR_UNSUPPORTED unless dtype is F16/BF16, head_size is 64, 128 or
- * 256, block_size is a power of two up to 256 and kv_len is below 2^31. Any GQA group query_heads / num_kv_heads:
+ * F16/BF16 caches: Q is rounded to the cache dtype and the softmax weights to
+ * the cache dtype before the MFMA products; accumulation and softmax are
+ * FP32. F32 caches: FP32 MFMAs on Q, K, V and the weights as they are (the
+ * 1e-5 contract of kvflux_paged_prefill_exact, head_size 64 or 128).
+ * KVFLUX_ERR_UNSUPPORTED unless head_size is 64, 128 or 256 (F32: 64 or
+ * 128), block_size is a power of two up to 256 and kv_len is below 2^31. Any GQA group query_heads / num_kv_heads:
  * groups 1..8 (and 16 at head_size 64/128) in one launch, others as one
  * launch per sub-group of heads (the largest divisor of the group among
  * 16, 8, 7, ..., 1 that one launch takes).
@@ -226,6 +228,7 @@ int kvflux_paged_prefill_split(const void* key_cache, const void* value_cache,
  * folded in) and the softmax weights enter the MFMAs as three 16-bit parts
  * each, so every product is exact in FP32, and the row sums are FP32 sums of
  * the weights. About three times the MFMA work of kvflux_paged_prefill_split.
+ * F32 caches run the FP32-MFMA prefill, as in kvflux_paged_prefill_split.
  * Same arguments, workspace and errors, except that head_size must be 64 or
  * 128 (256: KVFLUX_ERR_UNSUPPORTED). Replaces paged_attention_kernel
  * (reference src/v2/paged_attention.cu:108-128, 193-246) for the

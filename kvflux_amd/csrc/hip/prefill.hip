@@ -51,6 +51,7 @@ typedef __attribute__((ext_vector_type(2))) _Float16 pf_f16x2_t;
 struct PfBf16 {
     using Vec = pf_bf16x8_t;
     static constexpr bool kExact = false;
+    static constexpr bool kF32 = false;
     static constexpr std::uint32_t kOnes = 0x3f803f80u;  // two 1.0
     __device__ static std::uint32_t pack(float a, float b) {
         return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_bf16x2_t));
@@ -71,6 +72,7 @@ struct PfBf16 {
 struct PfF16 {
     using Vec = pf_f16x8_t;
     static constexpr bool kExact = false;
+    static constexpr bool kF32 = false;
     static constexpr std::uint32_t kOnes = 0x3c003c00u;  // two 1.0
     __device__ static std::uint32_t pack(float a, float b) {
         return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(pf_f32x2_t{a, b}, pf_f16x2_t));
@@ -96,6 +98,19 @@ struct PfBf16Exact : PfBf16 {
 };
 struct PfF16Exact : PfF16 {
     static constexpr bool kExact = true;
+};
+// FP32 caches: K, V, Q and the weights enter v_mfma_f32_16x16x4_f32 as they
+// are (exact products, FP32 accumulation), with the exact variants' FP32 row
+// sums and one row block per wavefront. Vec only sizes the 16-bit operand
+// arrays, which this policy leaves unused.
+struct PfF32 {
+    using Vec = pf_bf16x8_t;
+    static constexpr bool kExact = true;
+    static constexpr bool kF32 = true;
+    static constexpr std::uint32_t kOnes = 0;
+    __device__ static pf_f32x4_t mma4(float a, float b, const pf_f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
 };
 
 // NaN-propagating maximum of three (one v_maximum3_f32).
@@ -218,26 +233,29 @@ template <typename E, int kD, int kG>
 __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams p) {
     using M = E;
     using Vec = typename M::Vec;
-    constexpr int kSteps = kD / 32;            // K-dim steps of S^T
+    constexpr bool kF32 = E::kF32;
+    constexpr int kSteps = kD / 32;            // K-dim steps of S^T (16-bit)
+    constexpr int kQuads = kD / 16;            // 16-dim chunks of S^T (FP32: four MFMAs each)
     constexpr int kDt = kD / 16;               // dim blocks of O^T
-    constexpr int kCpr = kD / 8;               // 16-byte chunks per key row
-    constexpr int kRowBytes = kD * 2;
+    constexpr int kRowBytes = kD * (kF32 ? 4 : 2);
+    constexpr int kCpr = kRowBytes / 16;       // 16-byte chunks per key row
     constexpr int kTileBytes = kPfTile * kRowBytes;
     constexpr int kDma = kTileBytes / (kPfThreads * 16);  // tile loads per thread per cache
     constexpr int kPfNt = pf_blocks<E, kD>();
     constexpr bool kExact = E::kExact;
-    constexpr int kParts = kExact ? 3 : 1;  // 16-bit parts of Q and of the weights
+    constexpr int kParts = kExact && !kF32 ? 3 : 1;  // 16-bit parts of Q and of the weights
     constexpr int kBlocks = kPfWaves * kPfNt;   // 16-row blocks per workgroup
     constexpr int kTok = 16 * (kBlocks / kG);  // query tokens per workgroup
-    constexpr int kVSwz = kCpr / 8;            // V slot swizzle multiplier
+    constexpr int kVSwz = kF32 ? 0 : kCpr / 8;  // V slot swizzle multiplier (FP32 V rows are read straight)
     constexpr float kLazy = 8.0f;
     static_assert(kDma >= 1 && kTileBytes % (kPfThreads * 16) == 0, "tile split");
     static_assert(kG >= 1 && kG <= kBlocks, "a row block per head of the group");
+    static_assert(!kF32 || kD <= 128, "FP32 tiles of head_size 256 exceed the LDS");
 
-    __shared__ __attribute__((aligned(16))) std::uint16_t ktile0[kPfTile * kD];
-    __shared__ __attribute__((aligned(16))) std::uint16_t ktile1[kPfTile * kD];
-    __shared__ __attribute__((aligned(16))) std::uint16_t vtile0[kPfTile * kD];
-    __shared__ __attribute__((aligned(16))) std::uint16_t vtile1[kPfTile * kD];
+    __shared__ __attribute__((aligned(16))) std::uint16_t ktile0[kTileBytes / 2];
+    __shared__ __attribute__((aligned(16))) std::uint16_t ktile1[kTileBytes / 2];
+    __shared__ __attribute__((aligned(16))) std::uint16_t vtile0[kTileBytes / 2];
+    __shared__ __attribute__((aligned(16))) std::uint16_t vtile1[kTileBytes / 2];
     __shared__ std::uint32_t pages[pf_table_max<kD>()];
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
@@ -297,7 +315,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     };
     // The query rows' loads go out before the page list's, so the two round
     // trips overlap; the rows are rounded to the cache dtype after.
-    float4 qraw[kPfNt][kSteps][2];
+    // 16-bit caches: float4 pairs 2kk, 2kk + 1 are dims 32kk + 8quad .. +8 of
+    // the row; FP32: float4 c is dims 16c + 4quad .. +4.
+    float4 qraw[kPfNt][kQuads];
     std::uint32_t row_token[kPfNt];
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
@@ -309,33 +329,44 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         const float* src =
             query + (static_cast<std::uint64_t>(tq_safe) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
 #pragma unroll
-        for (int kk = 0; kk < kSteps; ++kk) {
-            qraw[n][kk][0] = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8);
-            qraw[n][kk][1] = *reinterpret_cast<const float4*>(src + kk * 32 + quad * 8 + 4);
+        for (int c = 0; c < kQuads; ++c) {
+            const int off = kF32 ? 16 * c + 4 * quad : 32 * (c / 2) + 8 * quad + 4 * (c % 2);
+            qraw[n][c] = *reinterpret_cast<const float4*>(src + off);
         }
     }
     stage(first_page(tile_begin & ~win_mask));
-    Vec qb_op[kParts][kPfNt][kSteps];
+    // FP32: Q * scale as it is, lane (quad, col) dims 16c + 4quad + j in qf[n][c][j].
+    pf_f32x4_t qf[kF32 ? kPfNt : 1][kF32 ? kQuads : 1];
+    Vec qb_op[kParts][kF32 ? 1 : kPfNt][kF32 ? 1 : kSteps];
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
+        if constexpr (kF32) {
 #pragma unroll
-        for (int kk = 0; kk < kSteps; ++kk) {
-            const float4 lo = qraw[n][kk][0], hi = qraw[n][kk][1];
-            const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            std::uint32_t w[kParts][4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if constexpr (kExact) {
-                    std::uint32_t parts[3];
-                    M::split3(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2, parts);
-#pragma unroll
-                    for (int k = 0; k < kParts; ++k) w[k][e] = parts[k];
-                } else {
-                    w[0][e] = M::pack(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2);
-                }
+            for (int c = 0; c < kQuads; ++c) {
+                const float4 v = qraw[n][c];
+                qf[n][c] = pf_f32x4_t{v.x, v.y, v.z, v.w} * p.scale_log2;
             }
+        } else {
 #pragma unroll
-            for (int k = 0; k < kParts; ++k) qb_op[k][n][kk] = __builtin_bit_cast(Vec, make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]));
+            for (int kk = 0; kk < kSteps; ++kk) {
+                const float4 lo = qraw[n][2 * kk], hi = qraw[n][2 * kk + 1];
+                const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                std::uint32_t w[kParts][4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (kExact) {
+                        std::uint32_t parts[3];
+                        M::split3(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2, parts);
+#pragma unroll
+                        for (int k = 0; k < kParts; ++k) w[k][e] = parts[k];
+                    } else {
+                        w[0][e] = M::pack(v[2 * e] * p.scale_log2, v[2 * e + 1] * p.scale_log2);
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < kParts; ++k)
+                    qb_op[k][n][kk] = __builtin_bit_cast(Vec, make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]));
+            }
         }
     }
     __syncthreads();  // pages[] ready (the query loads are complete as well)
@@ -351,7 +382,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     const std::uint32_t page_bytes = (static_cast<std::uint32_t>(kRowBytes) << p.bs_shift) * p.heads;
     const std::uint32_t head_bytes = (kvh << p.bs_shift) * kRowBytes;
     const std::uint32_t in_page_mask = (1u << p.bs_shift) - 1;
-    auto kswz = [](int row) { return kCpr == 16 ? (row & 15) : ((row >> 1) & 7); };
+    auto kswz = [](int row) { return kCpr >= 16 ? (row & 15) : ((row >> 1) & 7); };
     auto vswz = [](int row) { return kVSwz * (row & 7); };
     auto issue = [&](std::uint32_t tile, auto buf) {
         // Key tile * 64 + row: page (tile * 64 >> bs_shift) + (row >> bs_shift)
@@ -447,10 +478,35 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4_t*)(vbase + off + 16 * kRowBytes));
                 return __builtin_bit_cast(Vec, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             };
-            constexpr bool kEarlyV = kD == 128;
+            constexpr bool kEarlyV = kD == 128 && !kF32;
             Vec vop[kEarlyV ? kDt : 1];
             set_priority<1>();
-            {
+            if constexpr (kF32) {
+                // MFMA (c, j) takes, in lane (quad, col), dim 16c + 4quad + j of
+                // key col (K, one 16-byte read per c) and of row col (Q); the
+                // dim order does not change the sum.
+#pragma unroll
+                for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+                    for (int n = 0; n < kPfNt; ++n) s[kt2][n] = nref[n];
+#pragma unroll
+                for (int c = 0; c < kQuads; ++c) {
+                    float4 a[2];
+#pragma unroll
+                    for (int kt2 = 0; kt2 < 2; ++kt2)
+                        a[kt2] = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(kt) +
+                                                                  (32 * h + 16 * kt2) * kRowBytes + (k_read0 ^ (c << 6)));
+#pragma unroll
+                    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+                        for (int n = 0; n < kPfNt; ++n) {
+                            s[kt2][n] = M::mma4(a[kt2].x, qf[n][c][0], s[kt2][n]);
+                            s[kt2][n] = M::mma4(a[kt2].y, qf[n][c][1], s[kt2][n]);
+                            s[kt2][n] = M::mma4(a[kt2].z, qf[n][c][2], s[kt2][n]);
+                            s[kt2][n] = M::mma4(a[kt2].w, qf[n][c][3], s[kt2][n]);
+                        }
+                }
+            } else {
                 Vec a[kSteps][2];
 #pragma unroll
                 for (int kk = 0; kk < kSteps; ++kk)
@@ -520,47 +576,80 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                 }
                 have_ref = true;
             }
-            Vec pb[kParts][kPfNt];
+            if constexpr (kF32) {
+                // O^T += V^T P^T over keys: MFMA (kt2, r, g, j) takes key
+                // 16kt2 + 4quad + r in lane (quad, col), the weight the lane
+                // holds, and V dim 64g + 4col + j (one 16-byte read of the key's
+                // row per g). acc[4g + j][n][i] is then dim 64g + 16quad + 4i + j
+                // of row col.
+                const char* vrow = reinterpret_cast<const char*>(vt) + (32 * h + 4 * quad) * kRowBytes + 16 * col;
 #pragma unroll
-            for (int n = 0; n < kPfNt; ++n) {
-                float pr[8];
+                for (int kt2 = 0; kt2 < 2; ++kt2) {
+                    float pr[kPfNt][4];
 #pragma unroll
-                for (int kt2 = 0; kt2 < 2; ++kt2)
+                    for (int n = 0; n < kPfNt; ++n) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) pr[4 * kt2 + r] = __builtin_amdgcn_exp2f(s[kt2][n][r]);
-                std::uint32_t w[kParts][4];
-                if constexpr (kExact) {
-                    lsum[n][0] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        std::uint32_t parts[3];
-                        M::split3(pr[2 * j], pr[2 * j + 1], parts);
-#pragma unroll
-                        for (int k = 0; k < kParts; ++k) w[k][j] = parts[k];
+                        for (int r = 0; r < 4; ++r) pr[n][r] = __builtin_amdgcn_exp2f(s[kt2][n][r]);
+                        lsum[n][0] += (pr[n][0] + pr[n][1]) + (pr[n][2] + pr[n][3]);
                     }
-                } else {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) w[0][j] = M::pack(pr[2 * j], pr[2 * j + 1]);
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int g = 0; g < kD / 64; ++g) {
+                            const float4 v =
+                                *reinterpret_cast<const float4*>(vrow + (16 * kt2 + r) * kRowBytes + 256 * g);
+#pragma unroll
+                            for (int n = 0; n < kPfNt; ++n) {
+                                acc[4 * g][n] = M::mma4(v.x, pr[n][r], acc[4 * g][n]);
+                                acc[4 * g + 1][n] = M::mma4(v.y, pr[n][r], acc[4 * g + 1][n]);
+                                acc[4 * g + 2][n] = M::mma4(v.z, pr[n][r], acc[4 * g + 2][n]);
+                                acc[4 * g + 3][n] = M::mma4(v.w, pr[n][r], acc[4 * g + 3][n]);
+                            }
+                        }
+                }
+            } else {
+                Vec pb[kParts][kPfNt];
+#pragma unroll
+                for (int n = 0; n < kPfNt; ++n) {
+                    float pr[8];
+#pragma unroll
+                    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) pr[4 * kt2 + r] = __builtin_amdgcn_exp2f(s[kt2][n][r]);
+                    std::uint32_t w[kParts][4];
+                    if constexpr (kExact) {
+                        lsum[n][0] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            std::uint32_t parts[3];
+                            M::split3(pr[2 * j], pr[2 * j + 1], parts);
+#pragma unroll
+                            for (int k = 0; k < kParts; ++k) w[k][j] = parts[k];
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) w[0][j] = M::pack(pr[2 * j], pr[2 * j + 1]);
+                    }
+#pragma unroll
+                    for (int k = 0; k < kParts; ++k) pb[k][n] = __builtin_bit_cast(Vec, make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]));
                 }
 #pragma unroll
-                for (int k = 0; k < kParts; ++k) pb[k][n] = __builtin_bit_cast(Vec, make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]));
-            }
+                for (int dt = 0; dt < kDt; ++dt) {
+                    Vec a;
+                    if constexpr (kEarlyV) {
+                        a = vop[dt];
+                    } else {
+                        a = read_v(dt);
+                    }
 #pragma unroll
-            for (int dt = 0; dt < kDt; ++dt) {
-                Vec a;
-                if constexpr (kEarlyV) {
-                    a = vop[dt];
-                } else {
-                    a = read_v(dt);
+                    for (int n = 0; n < kPfNt; ++n)
+#pragma unroll
+                        for (int k = 0; k < kParts; ++k) acc[dt][n] = M::mma(a, pb[k][n], acc[dt][n]);
                 }
+                if constexpr (!kExact) {
 #pragma unroll
-                for (int n = 0; n < kPfNt; ++n)
-#pragma unroll
-                    for (int k = 0; k < kParts; ++k) acc[dt][n] = M::mma(a, pb[k][n], acc[dt][n]);
-            }
-            if constexpr (!kExact) {
-#pragma unroll
-                for (int n = 0; n < kPfNt; ++n) lsum[n] = M::mma(ones, pb[0][n], lsum[n]);
+                    for (int n = 0; n < kPfNt; ++n) lsum[n] = M::mma(ones, pb[0][n], lsum[n]);
+                }
             }
         }
     };
@@ -629,10 +718,20 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             const std::uint64_t prow = static_cast<std::uint64_t>(split) * tq * p.query_heads + row;
             float* dst = whole ? output + row * kD : p.part_o + prow * kD;
             const float sc = whole ? inv : 1.0f;
+            if constexpr (kF32) {
 #pragma unroll
-            for (int dt = 0; dt < kDt; ++dt) {
-                *reinterpret_cast<float4*>(dst + 16 * dt + 4 * quad) =
-                    make_float4(acc[dt][n][0] * sc, acc[dt][n][1] * sc, acc[dt][n][2] * sc, acc[dt][n][3] * sc);
+                for (int g = 0; g < kD / 64; ++g)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        *reinterpret_cast<float4*>(dst + 64 * g + 16 * quad + 4 * i) =
+                            make_float4(acc[4 * g][n][i] * sc, acc[4 * g + 1][n][i] * sc, acc[4 * g + 2][n][i] * sc,
+                                        acc[4 * g + 3][n][i] * sc);
+            } else {
+#pragma unroll
+                for (int dt = 0; dt < kDt; ++dt) {
+                    *reinterpret_cast<float4*>(dst + 16 * dt + 4 * quad) =
+                        make_float4(acc[dt][n][0] * sc, acc[dt][n][1] * sc, acc[dt][n][2] * sc, acc[dt][n][3] * sc);
+                }
             }
             // An empty split leaves l = 0; the combine skips it.
             if (!whole && quad == 0) *reinterpret_cast<float2*>(p.part_ml + 2 * prow) = make_float2(-nref[n][0], l);
@@ -810,11 +909,13 @@ int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_b
         return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill: block table shorter than kv_len");
     }
     const std::uint64_t group = query_heads / num_kv_heads;
-    if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128 && head_size != 256) || !is_pow2(block_size) ||
-        block_size > 256 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0x7fffffffULL ||
-        query_heads > 0xffffffffULL || num_kv_heads * block_size * head_size * 2 > 0xffffffffULL) {
+    if ((head_size != 64 && head_size != 128 && head_size != 256) || !is_pow2(block_size) || block_size > 256 ||
+        num_blocks > 0x7fffffffULL || num_kv_heads > 65535 || kv_len > 0x7fffffffULL || query_heads > 0xffffffffULL ||
+        num_kv_heads * block_size * head_size * dtype_bytes(dtype) > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: shape not handled by the MFMA kernel");
     }
+    // FP32 caches always take the FP32 MFMAs, whose products are exact.
+    if (dtype == KVFLUX_DTYPE_F32) exact = true;
     if (exact && head_size == 256) return fail(KVFLUX_ERR_UNSUPPORTED, "exact paged prefill: head_size 256");
 
     PrefillParams p{};
@@ -851,6 +952,7 @@ int paged_prefill(const void* key_cache, const void* value_cache, uint64_t num_b
     }
     const hipStream_t s = as_stream(stream);
     const std::uint32_t g = static_cast<std::uint32_t>(group);
+    if (dtype == KVFLUX_DTYPE_F32) return launch_prefill_head_size<PfF32>(p, head_size, g, s);
     if (exact) {
         if (dtype == KVFLUX_DTYPE_BF16) return launch_prefill_head_size<PfBf16Exact>(p, head_size, g, s);
         return launch_prefill_head_size<PfF16Exact>(p, head_size, g, s);
@@ -927,10 +1029,10 @@ extern "C" int kvflux_paged_prefill_batch(const void* key_cache, const void* val
     if (max_blocks_per_seq * block_size < max_kv_len) {
         return fail(KVFLUX_ERR_INVALID_ARGUMENT, "paged prefill batch: table rows shorter than max_kv_len");
     }
-    if (dtype == KVFLUX_DTYPE_F32 || (head_size != 64 && head_size != 128 && head_size != 256) ||
+    if ((head_size != 64 && head_size != 128 && head_size != 256) || (dtype == KVFLUX_DTYPE_F32 && head_size == 256) ||
         !is_pow2(block_size) || block_size > 256 || num_blocks > 0x7fffffffULL || num_kv_heads > 65535 ||
         max_kv_len > 0x7fffffffULL || query_heads > 0xffffffffULL || num_seqs > 0xffffffffULL ||
-        max_blocks_per_seq > 0xffffffffULL || num_kv_heads * block_size * head_size * 2 > 0xffffffffULL) {
+        max_blocks_per_seq > 0xffffffffULL || num_kv_heads * block_size * head_size * dtype_bytes(dtype) > 0xffffffffULL) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill batch: shape not handled by the MFMA kernel");
     }
     PrefillParams p{};
@@ -957,6 +1059,7 @@ extern "C" int kvflux_paged_prefill_batch(const void* key_cache, const void* val
     p.seq_q_offsets = query_offsets;
     const hipStream_t s = as_stream(stream);
     const std::uint32_t g = static_cast<std::uint32_t>(query_heads / num_kv_heads);
+    if (dtype == KVFLUX_DTYPE_F32) return launch_prefill_head_size<PfF32>(p, head_size, g, s);
     if (dtype == KVFLUX_DTYPE_BF16) return launch_prefill_head_size<PfBf16>(p, head_size, g, s);
     return launch_prefill_head_size<PfF16>(p, head_size, g, s);
 }

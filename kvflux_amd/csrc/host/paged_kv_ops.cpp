@@ -180,8 +180,9 @@ namespace {
 // kvflux_paged_prefill checks), so its workspace is reserved only for calls
 // that will use it.
 bool prefill_shape_ok(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len) {
-    if (query_tokens == 0 || layout.dtype() == DType::Float32) return false;
+    if (query_tokens == 0) return false;
     if (layout.head_size() != 64 && layout.head_size() != 128 && layout.head_size() != 256) return false;
+    if (layout.dtype() == DType::Float32 && layout.head_size() == 256) return false;
     const std::size_t bs = layout.block_size();
     if (bs > 256 || (bs & (bs - 1)) != 0) return false;  // a power of two up to 256
     return layout.num_blocks() <= 0x7fffffffULL && layout.num_kv_heads() <= 65535 && kv_len <= 0x7fffffffULL &&
@@ -189,6 +190,7 @@ bool prefill_shape_ok(const PagedKVLayout& layout, std::size_t query_tokens, std
 }
 
 // The rounded (2e-2) MFMA prefill: Fast, or Auto from 16 query tokens on.
+// FP32 caches take FP32 MFMAs there, whose products are exact.
 bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len,
                       AttentionPrecision precision) {
     if (precision == AttentionPrecision::Exact) return false;
@@ -197,7 +199,8 @@ bool prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens, std
 }
 
 // The exact (1e-5) MFMA prefill: Exact calls of 16 or more query tokens at
-// head_size 64 or 128 (fewer tokens run faster on the split-K kernel).
+// head_size 64 or 128, any cache dtype (fewer tokens run faster on the
+// split-K kernel).
 bool exact_prefill_eligible(const PagedKVLayout& layout, std::size_t query_tokens, std::size_t kv_len,
                             AttentionPrecision precision) {
     if (precision != AttentionPrecision::Exact || query_tokens < 16) return false;

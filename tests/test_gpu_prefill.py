@@ -147,8 +147,9 @@ def test_prefill_deterministic_and_unsupported(gpu):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     lib = capi.lib()
     td, qd, od = buffer_like(table), buffer_like(q), buffer_like(np.zeros(q.size, np.float32))
-    # FP32 caches, head_sizes 96 and 512 and block_size 48 are left to the exact kernels.
-    assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, bs, D, capi.DTYPE_F32, td.ptr, len(table), L, L,
+    # FP32 caches at head_size 256, head_sizes 96 and 512 and block_size 48
+    # are left to the split-K kernels.
+    assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, bs, 256, capi.DTYPE_F32, td.ptr, len(table), L, L,
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
     assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, H, bs, 96, capi.DTYPE_BF16, td.ptr, len(table), L, L,
                                     Hq, qd.ptr, od.ptr, None) == capi.ERR_UNSUPPORTED
@@ -507,3 +508,155 @@ def test_prefill_exact_matches_reference(gpu, name, kv_heads, q_heads, head_size
     assert lib.kvflux_paged_prefill_exact(kc.ptr, vc.ptr, blocks, kv_heads, bs, 256, CODES[name], td.ptr, len(table),
                                           kv_len, q_tokens, q_heads, qd.ptr, qd.ptr, None, 0,
                                           None) == capi.ERR_UNSUPPORTED
+
+
+F32_CASES = [  # kv_heads, q_heads, head_size, bs, kv_len, q_tokens
+    (2, 8, 128, 16, 1000, 1000),
+    (2, 8, 128, 16, 700, 37),
+    (1, 4, 64, 16, 600, 600),
+    (2, 6, 128, 32, 500, 500),      # group 6 (two idle blocks of eight)
+    (2, 32, 128, 16, 260, 260),     # group 16 as 2 x 8
+    (1, 12, 64, 64, 333, 333),      # group 12 as 2 x 6
+    (1, 4, 64, 1, 3000, 300),       # one-token pages
+    (2, 8, 128, 128, 1000, 1000),   # pages longer than a tile
+    (1, 2, 128, 2, 40, 40),         # two-token pages, one partial tile
+    (8, 32, 128, 16, 8192, 64),     # chunked prefill: keys split over workgroups
+    (1, 4, 128, 16, 40000, 16),     # page-list windows, split keys
+]
+
+
+def setup_f32(blocks, kv_heads, bs, head_size, kv_len, seed):
+    page = kv_heads * bs * head_size
+    kc = device.DeviceBuffer(blocks * page * 4)
+    vc = device.DeviceBuffer(blocks * page * 4)
+    device.fill_random(kc.ptr, blocks * page, oracle.F32, 1, seed * 3 + 1)
+    device.fill_random(vc.ptr, blocks * page, oracle.F32, 1, seed * 3 + 2)
+    npages = (kv_len + bs - 1) // bs
+    table = np.random.default_rng(seed).permutation(blocks)[:npages].astype(np.uint64)
+    return kc, vc, table
+
+
+@pytest.mark.parametrize("kv_heads,q_heads,head_size,bs,kv_len,q_tokens", F32_CASES)
+def test_prefill_f32_matches_reference(gpu, kv_heads, q_heads, head_size, bs, kv_len, q_tokens):
+    """FP32 caches on the MFMA prefill (FP32 MFMAs on Q, K, V and the weights
+    as they are, FP32 row sums): the whole output within the reference's 1e-5
+    of the oracle through all three single-sequence entry points, with and
+    without key splits; the split and exact entries give the same bits."""
+    blocks = (kv_len + bs - 1) // bs + 17
+    seed = kv_len + 7 * q_tokens
+    kc, vc, table = setup_f32(blocks, kv_heads, bs, head_size, kv_len, seed)
+    q = oracle.random_elements(0, q_tokens * q_heads * head_size, oracle.F32, 1, seed)
+    lib = capi.lib()
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_prefill_workspace_size(kv_heads, head_size, kv_len, q_tokens, q_heads, C.byref(ws)))
+    td, qd = buffer_like(table), buffer_like(q)
+    wd = device.DeviceBuffer(max(ws.value, 256))
+    outs = {}
+    for entry in ("plain", "split", "exact"):
+        od = buffer_like(np.full(q.size + 4, 777.0, np.float32))
+        if entry == "plain":
+            st = lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, capi.DTYPE_F32, td.ptr,
+                                          len(table), kv_len, q_tokens, q_heads, qd.ptr, od.ptr, None)
+        else:
+            fn = lib.kvflux_paged_prefill_split if entry == "split" else lib.kvflux_paged_prefill_exact
+            st = fn(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, capi.DTYPE_F32, td.ptr, len(table), kv_len,
+                    q_tokens, q_heads, qd.ptr, od.ptr, wd.ptr, ws.value, None)
+        assert st == 0, (entry, capi.last_error())
+        device.synchronize()
+        out = od.download(np.float32)
+        assert np.all(out[q.size:] == 777.0), entry
+        outs[entry] = out[:q.size]
+    assert np.array_equal(outs["split"].view(np.uint32), outs["exact"].view(np.uint32))
+    kh, vh = kc.download(np.float32), vc.download(np.float32)
+    exp = oracle.paged_attention_causal(kh, vh, kv_heads, bs, head_size, oracle.F32, table, kv_len, q, q_tokens,
+                                        q_heads, threads=8)
+    for entry, got in outs.items():
+        assert np.all(np.isfinite(got)), entry
+        assert np.abs(got - exp).max() < 1e-5, entry
+
+
+def test_prefill_f32_batch_and_cpp_routing(gpu, v2):
+    """kvflux_paged_prefill_batch on an FP32 cache gives each sequence the
+    bits of its own kvflux_paged_prefill call; the C++ paged_attention (the
+    reference's signature, and Auto) sends a 16-token FP32 call to the MFMA
+    prefill (the same bits as the C ABI call with a workspace) and a 15-token
+    one to the split-K kernel, both within 1e-5 of the oracle."""
+    lib = capi.lib()
+    kv_heads, q_heads, head_size, bs = 2, 8, 128, 16
+    seqs = [(700, 700), (1500, 64), (33, 33)]
+    n = len(seqs)
+    width = max((kv + bs - 1) // bs for kv, _ in seqs) + 2
+    blocks = n * width + 3
+    kc, vc, _ = setup_f32(blocks, kv_heads, bs, head_size, 1, 61)
+    order = np.random.default_rng(62).permutation(blocks).astype(np.uint64)
+    table = np.full((n, width), 2**64 - 1, np.uint64)
+    for i, (kv, _) in enumerate(seqs):
+        npg = (kv + bs - 1) // bs
+        table[i, :npg] = order[i * width:i * width + npg]
+    q_lens = np.array([ql for _, ql in seqs], np.uint64)
+    kv_lens = np.array([kv for kv, _ in seqs], np.uint64)
+    offsets = np.concatenate([[0], np.cumsum(q_lens + 1)[:-1]]).astype(np.uint64)
+    rows_total = int(offsets[-1] + q_lens[-1] + 1)
+    row = q_heads * head_size
+    q = oracle.random_elements(0, rows_total * row, oracle.F32, 1, 63)
+    td, qd = buffer_like(table.reshape(-1)), buffer_like(q)
+    kd, ld, od_ = buffer_like(kv_lens), buffer_like(q_lens), buffer_like(offsets)
+    out = buffer_like(np.full(rows_total * row, 555.0, np.float32))
+    assert lib.kvflux_paged_prefill_batch(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, capi.DTYPE_F32, td.ptr,
+                                          width, kd.ptr, ld.ptr, od_.ptr, n, int(q_lens.max()), int(kv_lens.max()),
+                                          q_heads, qd.ptr, out.ptr, None) == 0, capi.last_error()
+    device.synchronize()
+    got = out.download(np.float32).reshape(rows_total, row)
+    kh, vh = kc.download(np.float32), vc.download(np.float32)
+    used = np.zeros(rows_total, bool)
+    for i, (kv, ql) in enumerate(seqs):
+        o0 = int(offsets[i])
+        used[o0:o0 + ql] = True
+        qi = q.reshape(rows_total, row)[o0:o0 + ql].reshape(-1)
+        sd, so = buffer_like(table[i]), buffer_like(np.zeros(qi.size, np.float32))
+        qs = buffer_like(qi)
+        assert lib.kvflux_paged_prefill(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, capi.DTYPE_F32, sd.ptr,
+                                        width, kv, ql, q_heads, qs.ptr, so.ptr, None) == 0, capi.last_error()
+        device.synchronize()
+        assert np.array_equal(got[o0:o0 + ql].reshape(-1).view(np.uint32), so.download(np.float32).view(np.uint32))
+        exp = oracle.paged_attention_causal(kh, vh, kv_heads, bs, head_size, oracle.F32, table[i], kv, qi, ql,
+                                            q_heads, threads=8)
+        assert np.abs(got[o0:o0 + ql].reshape(-1) - exp).max() < 1e-5, i
+    assert np.all(got[~used] == 555.0)
+
+    pool = v2.PhysicalBlockPool(64, 16)
+    storage = v2.PagedKVStorage(pool, 2, 128, v2.DType.Float32)
+    seq = v2.SequenceState(1, pool)
+    seq.append_tokens(300)
+    count = storage.layout().cache_bytes() // 4
+    device.fill_random(storage.key_base(), count, oracle.F32, 1, 64)
+    device.fill_random(storage.value_base(), count, oracle.F32, 1, 65)
+    kh = device.memcpy_d2h(storage.key_base(), storage.layout().cache_bytes(), np.float32)
+    vh = device.memcpy_d2h(storage.value_base(), storage.layout().cache_bytes(), np.float32)
+    rtable = np.array(v2.build_read_block_table(seq), np.uint64)
+    P = v2.AttentionPrecision
+    for q_tokens in (15, 16):
+        q = oracle.random_elements(0, q_tokens * 8 * 128, oracle.F32, 1, 66 + q_tokens)
+        qd = buffer_like(q)
+        res = {}
+        for prec in (None, P.Auto, P.Fast):
+            od = buffer_like(np.zeros(q.size, np.float32))
+            if prec is None:
+                v2.paged_attention(storage, seq, qd.ptr, od.ptr, q_tokens, 8)
+            else:
+                v2.paged_attention(storage, seq, qd.ptr, od.ptr, q_tokens, 8, prec)
+            res[prec] = od.download(np.float32)
+        assert np.array_equal(res[None].view(np.uint32), res[P.Auto].view(np.uint32)), q_tokens
+        exp = oracle.paged_attention_causal(kh, vh, 2, 16, 128, oracle.F32, rtable, 300, q, q_tokens, 8)
+        assert np.abs(res[None] - exp).max() < 1e-5, q_tokens
+        assert np.abs(res[P.Fast] - exp).max() < 1e-5, q_tokens
+        ws = C.c_size_t(0)
+        capi.check(lib.kvflux_paged_prefill_workspace_size(2, 128, 300, q_tokens, 8, C.byref(ws)))
+        wd = device.DeviceBuffer(max(ws.value, 256))
+        td, od = buffer_like(rtable), buffer_like(np.zeros(q.size, np.float32))
+        assert lib.kvflux_paged_prefill_exact(storage.key_base(), storage.value_base(), 64, 2, 16, 128,
+                                              capi.DTYPE_F32, td.ptr, len(rtable), 300, q_tokens, 8, qd.ptr, od.ptr,
+                                              wd.ptr, ws.value, None) == 0
+        device.synchronize()
+        same = np.array_equal(od.download(np.float32).view(np.uint32), res[None].view(np.uint32))
+        assert same == (q_tokens >= 16), q_tokens

@@ -186,9 +186,9 @@ def write_gather_case(rng, i):
 
 def exact_prefill_case(rng, i):
     """kvflux_paged_prefill_exact on one sequence (a whole prompt or a
-    trailing chunk, with its workspace so keys may split): every output
-    against the oracle at 1e-5."""
-    name = ("BFloat16", "Float16")[int(rng.integers(2))]
+    trailing chunk, with its workspace so keys may split; 16-bit or FP32
+    caches): every output against the oracle at 1e-5."""
+    name = ("BFloat16", "Float16", "Float32")[int(rng.integers(3))]
     D = int(rng.choice([64, 128]))
     H = int(rng.choice([1, 2, 4]))
     Hq = H * int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 16]))
@@ -197,11 +197,12 @@ def exact_prefill_case(rng, i):
     ql = kv if rng.random() < 0.5 else int(rng.integers(16, kv + 1))
     while ql * kv * Hq * D > 2e9:  # bound the oracle's work
         ql = max(16, ql // 2)
-    code = DTYPES[name][0]
+    code, host = DTYPES[name]
+    esize = np.dtype(host).itemsize
     npg = (kv + bs - 1) // bs
     blocks = npg + 5
     page = H * bs * D
-    kc, vc = device.DeviceBuffer(blocks * page * 2), device.DeviceBuffer(blocks * page * 2)
+    kc, vc = device.DeviceBuffer(blocks * page * esize), device.DeviceBuffer(blocks * page * esize)
     device.fill_random(kc.ptr, blocks * page, code, 1, 7000 + i)
     device.fill_random(vc.ptr, blocks * page, code, 1, 8000 + i)
     table = rng.permutation(blocks)[:npg].astype(np.uint64)
@@ -218,7 +219,7 @@ def exact_prefill_case(rng, i):
     out = od.download(np.float32)
     cfg = f"exact prefill {name} D={D} H={H} Hq={Hq} bs={bs} kv={kv} q={ql}"
     assert np.all(out[q.size:] == 555.0), cfg
-    exp = oracle.paged_attention_causal(kc.download(np.uint16), vc.download(np.uint16), H, bs, D, code, table, kv, q,
+    exp = oracle.paged_attention_causal(kc.download(host), vc.download(host), H, bs, D, code, table, kv, q,
                                         ql, Hq, threads=8)
     err = float(np.abs(out[:q.size] - exp).max())
     assert err < 1e-5, (cfg, err)
