@@ -1,4 +1,5 @@
-// Causal paged prefill on MFMA (gfx950): BF16/FP16 caches, head_size 64/128/256.
+// Causal paged prefill on MFMA (gfx950): BF16/FP16 caches, head_size 64/128/256,
+// and FP32 caches, head_size 64/128 (v_mfma_f32_16x16x4_f32, see PfF32).
 //
 // One workgroup (8 wavefronts, two per SIMD) owns one kv head and R row blocks
 // of 16 rows (R = 16; 8 at head_size 256), a row being a (query token, query
