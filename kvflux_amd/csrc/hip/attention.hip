@@ -521,7 +521,7 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 
 // ---------------------------------------------------------------- block_size 16 decode
 // Hot path for head_size 64/128: 16-bit caches with pages of 1 to 128 tokens,
-// FP32 caches with pages of 16 to 128 tokens:
+// FP32 caches with pages of 16 to 128 tokens (1 to 128 at head_size 64):
 //  * persistent workgroups walk a plan of (row, chunk, kv head) items built
 //    in LDS from the row lengths (exclusive prefix of chunk counts), so no
 //    workgroup is launched for an empty chunk and consecutive items read the
@@ -610,7 +610,6 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
     // FP32 caches: QK^T and P*V on v_mfma_f32_16x16x4_f32 with FP32 K, V, Q
     // and weights as they are (no splits, no LDS staging of V).
     constexpr bool kF32 = std::is_same<E, F32>::value;
-    static_assert(!(kF32 && kSmall), "FP32 caches take pages of 16 tokens or more");
     using M = Mfma<typename std::conditional<kF32, Bf16, E>::type>;
     using Vec = typename M::Vec;
     using T = typename E::Storage;
@@ -852,6 +851,24 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p
         const std::uint32_t first = jt << tps;
         const std::uint32_t bs_mask = (1u << bs_shift) - 1;
         const std::uint64_t head = kvh * head_stride;
+        if constexpr (kF32) {
+            // The lanes of load(), each token row from its own page slot.
+            {
+                const std::uint32_t t = static_cast<std::uint32_t>(col);
+                const T* kb = kc + slot_offset(pages, first + (t >> bs_shift)) + head + (t & bs_mask) * kD + quad * 4;
+#pragma unroll
+                for (int m = 0; m < kF32Chunks; ++m) b.k[m] = *reinterpret_cast<const uint4*>(kb + 16 * m);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const std::uint32_t t = static_cast<std::uint32_t>(4 * quad + kk);
+                const T* vb = vc + slot_offset(pages, first + (t >> bs_shift)) + head + (t & bs_mask) * kD + col * 4;
+#pragma unroll
+                for (int mm = 0; mm < kD / 64; ++mm)
+                    b.v[kk * (kD / 64) + mm] = stream_load(reinterpret_cast<const uint4*>(vb + 64 * mm));
+            }
+            return;
+        }
         {
             const std::uint32_t t = static_cast<std::uint32_t>(col);
             const T* kb = kc + slot_offset(pages, first + (t >> bs_shift)) + head + (t & bs_mask) * kD + quad * 8;
@@ -1508,8 +1525,9 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             if (small && kD == 128 && sub > kSmallMaxGroup128) return plan_fallback(group, max_chunks, plan);
             int slots = 0;
             int status = KVFLUX_OK;
-            if constexpr (std::is_same<E, F32>::value) {
-                // FP32 caches: pages of 16 tokens or more (FP32 MFMA path).
+            if constexpr (std::is_same<E, F32>::value && kD == 128) {
+                // FP32 at head_size 128: pages of 16 tokens or more (with small
+                // pages' per-lane page addresses it would spill).
                 if (small) return plan_fallback(group, max_chunks, plan);
                 status = resident_slots_for<E, kD, false>(sub, &slots);
             } else {
@@ -1610,8 +1628,8 @@ template <typename E, int kD, int kG>
 int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
     p.row_base = 0;
     if (plan.small) {
-        if constexpr (std::is_same<E, F32>::value) {
-            return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: FP32 caches with pages under 16 tokens");
+        if constexpr (std::is_same<E, F32>::value && kD == 128) {
+            return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: FP32 caches at head_size 128 with pages under 16 tokens");
         } else if constexpr (kD != 128 || kG <= static_cast<int>(kSmallMaxGroup128)) {
             hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, true>), dim3(plan.grid), dim3(kThreads), 0, s, p);
         } else {

@@ -358,7 +358,11 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
     ("BFloat16", 4, 64, 4, 28),   # group 7 at head_size 64 on the small-page kernel
     ("Float32", 32, 128, 2, 8),
     ("Float32", 64, 64, 2, 12),
-    ("Float32", 8, 128, 2, 8),    # FP32 with pages under 16 tokens stays on the split kernel
+    ("Float32", 8, 128, 2, 8),    # FP32 at head_size 128 with pages under 16 tokens: split kernel
+    ("Float32", 8, 64, 2, 8),     # FP32 at head_size 64: small pages on the FP32 MFMA kernel
+    ("Float32", 4, 64, 1, 5),
+    ("Float32", 2, 64, 2, 16),
+    ("Float32", 1, 64, 1, 8),
 ]
 
 
@@ -367,8 +371,9 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     """Pages of 32, 64 and 128 tokens run on the block-size-16 kernel as
     16-token tiles (a contiguous part of one kv head's rows of a page);
     pages of 1, 2, 4 and 8 tokens too, each 16-token tile gathering its rows
-    from 16 / block_size pages (groups above 5 at head_size 128 stay on the
-    split kernel). Lengths sit on tile and page boundaries; table entries
+    from 16 / block_size pages (groups above 5 at head_size 128, and FP32
+    at head_size 128, stay on the split kernel). Lengths sit on tile and page
+    boundaries; table entries
     past a row's pages are poisoned, so a tile's last pages can be missing.
     Matches the oracle at 1e-5, bit-identical on repeat."""
     lib = capi.lib()
@@ -408,7 +413,8 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     assert np.abs(outs[0] - exp).max() < TOL
 
 
-@pytest.mark.parametrize("name,bs,head_size", [("BFloat16", 8, 128), ("BFloat16", 1, 128), ("Float16", 4, 64)])
+@pytest.mark.parametrize("name,bs,head_size", [("BFloat16", 8, 128), ("BFloat16", 1, 128), ("Float16", 4, 64),
+                                               ("Float32", 2, 64)])
 def test_decode_small_pages_item_sizes(gpu, name, bs, head_size):
     """Small pages cap the work item at 256 * block_size tokens (the item's
     page slots fit one lane each): 128 rows of up to 20000 tokens with 4 kv
@@ -416,9 +422,10 @@ def test_decode_small_pages_item_sizes(gpu, name, bs, head_size):
     Sampled rows, including item boundaries, match the oracle at 1e-5."""
     lib = capi.lib()
     H, Hq, rows, max_len, P = 4, 16, 128, 20000, 8192
-    code = DTYPES[name][0]
+    code, host = DTYPES[name]
     page = H * bs * head_size
-    kc, vc = device.DeviceBuffer(P * page * 2), device.DeviceBuffer(P * page * 2)
+    esize = np.dtype(host).itemsize
+    kc, vc = device.DeviceBuffer(P * page * esize), device.DeviceBuffer(P * page * esize)
     device.fill_random(kc.ptr, P * page, code, 1, 51)
     device.fill_random(vc.ptr, P * page, code, 1, 52)
     rng = np.random.default_rng(bs * 131 + head_size)
@@ -442,7 +449,7 @@ def test_decode_small_pages_item_sizes(gpu, name, bs, head_size):
     got = od.download(np.float32).reshape(rows, -1)
     assert np.all(np.isfinite(got))
     sample = np.array(sorted(set(range(len(edges))) | set(rng.choice(rows, 5, replace=False).tolist())))
-    kh, vh = kc.download(np.uint16), vc.download(np.uint16)
+    kh, vh = kc.download(host), vc.download(host)
     exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table[sample].reshape(-1), width,
                                       lens[sample], q.reshape(rows, -1)[sample].reshape(-1), Hq, threads=8)
     assert np.abs(got[sample].reshape(-1) - exp).max() < TOL
