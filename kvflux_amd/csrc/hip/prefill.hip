@@ -1,13 +1,13 @@
 // Causal paged prefill on MFMA (gfx950): BF16/FP16 caches, head_size 64/128/256,
 // and FP32 caches, head_size 64/128 (v_mfma_f32_16x16x4_f32, see PfF32).
 //
-// One workgroup (8 wavefronts, two per SIMD) owns one kv head and R row blocks
-// of 16 rows (R = 16; 8 at head_size 256), a row being a (query token, query
-// head) pair of G query heads of that kv head: 16 * floor(R / G) tokens x G
-// heads (G <= 8, or 16 when R = 16; the row blocks past R / G * G idle when G
-// does not divide R; other GQA groups run as passes over sub-groups of G
-// heads). Wavefront w owns row blocks R/8 * w .. (row block b = head b % G,
-// tokens 16 * (b / G) ..). A call that would not fill the GPU (short query
+// One workgroup (8 wavefronts, two per SIMD) owns one kv head and 16 * R rows
+// (R = 16 row blocks of 16; 8 at head_size 256 and in the exact and FP32
+// variants), a row being a (query token, query head) pair of the G query heads
+// of that kv head: row r is head r % G of token r / G, so a workgroup takes
+// floor(16 * R / G) tokens of every head and at most G - 1 rows idle (a group
+// above 16 * R runs as passes over sub-groups of heads). Wavefront w owns row
+// blocks R/8 * w .. (rows 16 b .. 16 b + 15). A call that would not fill the GPU (short query
 // blocks against a long prefix) may spread each workgroup's keys over several
 // workgroups, merged by paged_prefill_combine_kernel. Keys stream through
 // LDS in tiles of 64, double-buffered: K and V go from global memory straight
@@ -172,6 +172,8 @@ struct PrefillParams {
     std::uint32_t query_heads;
     std::uint32_t q_group;    // query heads per kv head
     std::uint32_t q_first;    // first query head of the group this launch covers
+    std::uint32_t q_pass;     // query heads this launch covers (rows: token-major, head-minor)
+    std::uint32_t tok;        // query tokens per workgroup: floor(rows per workgroup / q_pass)
     std::uint32_t qblocks;    // ceil(tq / tokens per workgroup)
     const float* query;       // [tq][query_heads][D]
     float* output;            // [tq][query_heads][D]
@@ -230,7 +232,7 @@ __device__ inline void set_priority() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <typename E, int kD, int kG>
+template <typename E, int kD>
 __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams p) {
     using M = E;
     using Vec = typename M::Vec;
@@ -246,11 +248,9 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     constexpr bool kExact = E::kExact;
     constexpr int kParts = kExact && !kF32 ? 3 : 1;  // 16-bit parts of Q and of the weights
     constexpr int kBlocks = kPfWaves * kPfNt;   // 16-row blocks per workgroup
-    constexpr int kTok = 16 * (kBlocks / kG);  // query tokens per workgroup
     constexpr int kVSwz = kF32 ? 0 : kCpr / 8;  // V slot swizzle multiplier (FP32 V rows are read straight)
     constexpr float kLazy = 8.0f;
     static_assert(kDma >= 1 && kTileBytes % (kPfThreads * 16) == 0, "tile split");
-    static_assert(kG >= 1 && kG <= kBlocks, "a row block per head of the group");
     static_assert(!kF32 || kD <= 128, "FP32 tiles of head_size 256 exceed the LDS");
 
     __shared__ __attribute__((aligned(16))) std::uint16_t ktile0[kTileBytes / 2];
@@ -281,10 +281,10 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
         table = p.table + static_cast<std::uint64_t>(seq) * p.table_len;
         query = p.query + q0 * p.query_heads * kD;
         output = p.output + q0 * p.query_heads * kD;
-        if (tq == 0 || static_cast<std::uint64_t>(qb) * kTok >= tq) return;  // uniform
+        if (tq == 0 || static_cast<std::uint64_t>(qb) * p.tok >= tq) return;  // uniform
     }
-    const std::uint32_t t0 = qb * kTok;
-    const std::uint32_t t_end = t0 + kTok < tq ? t0 + kTok : tq;
+    const std::uint32_t t0 = qb * p.tok;
+    const std::uint32_t t_end = t0 + p.tok < tq ? t0 + p.tok : tq;
     const std::uint32_t past = kv_len - tq;
     const std::uint32_t last_key = past + t_end - 1;
     const std::uint32_t ntiles = last_key / kPfTile + 1;
@@ -319,13 +319,15 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     // 16-bit caches: float4 pairs 2kk, 2kk + 1 are dims 32kk + 8quad .. +8 of
     // the row; FP32: float4 c is dims 16c + 4quad .. +4.
     float4 qraw[kPfNt][kQuads];
-    std::uint32_t row_token[kPfNt];
+    std::uint32_t row_token[kPfNt], row_head[kPfNt];
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
-        const int b = wave * kPfNt + n;
-        const int g = b % kG;
-        const std::uint32_t token = t0 + 16 * (b / kG) + col;
+        // Row 16 b + col: head (16 b + col) % G of token (16 b + col) / G.
+        const std::uint32_t r = static_cast<std::uint32_t>(16 * (wave * kPfNt + n) + col);
+        const std::uint32_t g = r % p.q_pass;
+        const std::uint32_t token = t0 + r / p.q_pass;
         row_token[n] = token;
+        row_head[n] = g;
         const std::uint32_t tq_safe = token < tq ? token : tq - 1;
         const float* src =
             query + (static_cast<std::uint64_t>(tq_safe) * p.query_heads + kvh * p.q_group + p.q_first + g) * kD;
@@ -708,11 +710,10 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     for (int n = 0; n < kPfNt; ++n) {
         const float l = kExact ? sum_across_quads(lsum[n][0]) : lsum[n][0];
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        const int b = wave * kPfNt + n;
-        const int g = b % kG;
         const std::uint32_t token = row_token[n];
         if (token < t_end) {
-            const std::uint64_t row = static_cast<std::uint64_t>(token) * p.query_heads + kvh * p.q_group + p.q_first + g;
+            const std::uint64_t row =
+                static_cast<std::uint64_t>(token) * p.query_heads + kvh * p.q_group + p.q_first + row_head[n];
             // One store path for both cases (two would hold the accumulators
             // twice): normalised rows of the output, or unnormalised partials.
             const bool whole = p.splits == 1;
@@ -778,57 +779,42 @@ __global__ __launch_bounds__(256) void paged_prefill_combine_kernel(const float*
     }
 }
 
-template <typename E, int kD, int kG>
+// One launch over the heads q_first .. q_first + q_pass - 1 of every kv head.
+template <typename E, int kD>
 int launch_prefill_pass(const PrefillParams& p, hipStream_t s) {
     PrefillParams q = p;
-    constexpr unsigned kTok = 16 * (kPfWaves * pf_blocks<E, kD>() / kG);
+    constexpr unsigned kRows = 16 * kPfWaves * pf_blocks<E, kD>();
+    q.tok = kRows / p.q_pass;
     // tq: the query tokens of the sequence, or the most of any sequence of a batch.
-    q.qblocks = (p.tq + kTok - 1) / kTok;
+    q.qblocks = (p.tq + q.tok - 1) / q.tok;
     const std::uint64_t grid = static_cast<std::uint64_t>(q.qblocks) * p.heads * (p.num_seqs ? p.num_seqs : p.splits);
     if (grid > 0xffffffffULL) return fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: %llu workgroups",
                                           static_cast<unsigned long long>(grid));
-    hipLaunchKernelGGL((paged_prefill_kernel<E, kD, kG>), dim3(static_cast<unsigned>(grid)), dim3(kPfThreads), 0, s, q);
+    hipLaunchKernelGGL((paged_prefill_kernel<E, kD>), dim3(static_cast<unsigned>(grid)), dim3(kPfThreads), 0, s, q);
     return launch_status("paged_prefill_kernel");
 }
 
-// Query heads per workgroup pass for a GQA group, with `blocks` row blocks
-// per workgroup (16, or 8 at head_size 256): the group itself up to 8 and at
-// 16 when blocks allow, else the largest divisor of it among 16, 8, 7, ..., 1
-// that fits (then the group runs as group / sub passes over every kv head).
-inline std::uint32_t prefill_sub_group(std::uint32_t group, std::uint32_t blocks) {
-    if (group <= 8) return group;
-    if (blocks >= 16 && group % 16 == 0) return 16;
-    for (std::uint32_t d = 8; d > 1; --d)
+// Query heads per launch for a GQA group with `rows` rows per workgroup (256,
+// or 128 with one row block per wavefront): the whole group when it fits,
+// else the largest divisor of it that does (the group then runs as
+// group / sub launches over every kv head).
+inline std::uint32_t prefill_sub_group(std::uint32_t group, std::uint32_t rows) {
+    if (group <= rows) return group;
+    for (std::uint32_t d = rows; d > 1; --d)
         if (group % d == 0) return d;
     return 1;
 }
 
 template <typename E, int kD>
 int launch_prefill_group(const PrefillParams& p, std::uint32_t group, hipStream_t s) {
-    constexpr int kBlocks = kPfWaves * pf_blocks<E, kD>();
-    const std::uint32_t sub = prefill_sub_group(group, kBlocks);
+    constexpr std::uint32_t kRows = 16 * kPfWaves * pf_blocks<E, kD>();
+    const std::uint32_t sub = prefill_sub_group(group, kRows);
     PrefillParams q = p;
     q.q_group = group;
+    q.q_pass = sub;
     for (std::uint32_t first = 0; first < group; first += sub) {
         q.q_first = first;
-        int st = KVFLUX_OK;
-        switch (sub) {
-        case 1: st = launch_prefill_pass<E, kD, 1>(q, s); break;
-        case 2: st = launch_prefill_pass<E, kD, 2>(q, s); break;
-        case 3: st = launch_prefill_pass<E, kD, 3>(q, s); break;
-        case 4: st = launch_prefill_pass<E, kD, 4>(q, s); break;
-        case 5: st = launch_prefill_pass<E, kD, 5>(q, s); break;
-        case 6: st = launch_prefill_pass<E, kD, 6>(q, s); break;
-        case 7: st = launch_prefill_pass<E, kD, 7>(q, s); break;
-        case 8: st = launch_prefill_pass<E, kD, 8>(q, s); break;
-        default:
-            if constexpr (kBlocks >= 16) {
-                st = launch_prefill_pass<E, kD, 16>(q, s);
-            } else {
-                st = fail(KVFLUX_ERR_UNSUPPORTED, "paged prefill: sub-group %u", sub);
-            }
-            break;
-        }
+        const int st = launch_prefill_pass<E, kD>(q, s);
         if (st != KVFLUX_OK) return st;
     }
     if (p.splits > 1) {
@@ -869,9 +855,9 @@ struct PrefillPlan {
 inline PrefillPlan prefill_plan(std::uint64_t head_size, std::uint64_t group, std::uint64_t num_kv_heads,
                                 std::uint64_t kv_len, std::uint64_t query_tokens, std::uint64_t query_heads,
                                 bool exact = false) {
-    const std::uint64_t blocks = head_size == 256 || exact ? kPfWaves : 2 * kPfWaves;
-    const std::uint64_t sub = prefill_sub_group(static_cast<std::uint32_t>(group), static_cast<std::uint32_t>(blocks));
-    const std::uint64_t tok = 16 * (blocks / sub);
+    const std::uint64_t rows = 16 * (head_size == 256 || exact ? kPfWaves : 2 * kPfWaves);
+    const std::uint64_t sub = prefill_sub_group(static_cast<std::uint32_t>(group), static_cast<std::uint32_t>(rows));
+    const std::uint64_t tok = rows / sub;
     const std::uint64_t wgs = (query_tokens + tok - 1) / tok * num_kv_heads;
     const std::uint64_t tiles = (kv_len + kPfTile - 1) / kPfTile;
     std::uint64_t splits = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;

@@ -85,9 +85,9 @@ CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("Float16", 2, 4, 64, 16, 600, 600),
     ("BFloat16", 4, 4, 64, 64, 300, 300),
     ("Float16", 1, 2, 128, 16, 513, 100),
-    # GQA groups that do not divide 16 row blocks (idle blocks per workgroup),
-    # group 16 (one token block per workgroup), and groups run as passes over
-    # sub-groups: 10 -> 2 x 5, 11 -> 11 x 1, 12 -> 2 x 6, 32 -> 2 x 16.
+    # Rows are head-minor (row r: head r % G of token r / G), so any group up
+    # to 256 runs in one launch: groups that do not divide the 256 rows of a
+    # workgroup (up to G - 1 idle rows), and 10, 11, 12, 32 in one pass.
     ("BFloat16", 2, 6, 128, 16, 500, 500),
     ("Float16", 1, 5, 64, 32, 400, 170),
     ("BFloat16", 2, 12, 64, 16, 300, 300),
@@ -97,8 +97,8 @@ CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("BFloat16", 1, 11, 64, 16, 150, 150),
     ("Float16", 1, 12, 128, 64, 333, 333),
     ("BFloat16", 1, 32, 64, 16, 200, 200),
-    # head_size 256: 8 row blocks of 16 per workgroup (group 3 leaves 2 idle;
-    # group 16 runs as 2 x 8)
+    # head_size 256: 8 row blocks of 16 per workgroup (group 3 leaves 2 rows
+    # idle)
     ("BFloat16", 2, 2, 256, 16, 400, 400),
     ("Float16", 1, 3, 256, 32, 300, 120),
     ("BFloat16", 2, 8, 256, 16, 260, 260),
@@ -241,7 +241,8 @@ SPLIT_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("BFloat16", 2, 8, 128, 16, 5126, 100),    # split 16 starts at key 5120, inside the last
                                                # block's diagonal (rows 5090..5119 see none of it)
     ("Float16", 1, 16, 128, 16, 3000, 40),     # group 16, one token block per workgroup
-    ("BFloat16", 2, 20, 64, 32, 4000, 77),     # group 10 as 2 x 5 passes, then one combine
+    ("BFloat16", 2, 20, 64, 32, 4000, 77),     # group 10 in one launch, then one combine
+    ("BFloat16", 1, 300, 64, 16, 1000, 3),     # group 300 as 2 x 150 passes, then one combine
     ("BFloat16", 1, 2, 256, 16, 6000, 48),
     ("BFloat16", 1, 4, 128, 1, 20000, 16),     # page-list windows inside splits
     ("BFloat16", 2, 8, 128, 16, 3000, 1),      # one query token (Fast precision sends it here)
@@ -334,7 +335,8 @@ BATCH_CASES = [  # name, kv_heads, q_heads, head_size, bs, [(kv_len, q_len), ...
     ("BFloat16", 2, 8, 128, 16, [(700, 700), (1500, 1500), (64, 64), (1000, 37), (2049, 2049)]),
     ("Float16", 1, 5, 64, 4, [(300, 300), (257, 100), (33, 33)]),
     ("BFloat16", 2, 4, 256, 32, [(400, 400), (1200, 800)]),
-    ("BFloat16", 1, 12, 128, 1, [(200, 200), (150, 1)]),  # group 12 as two passes of 6
+    ("BFloat16", 1, 12, 128, 1, [(200, 200), (150, 1)]),  # group 12: 21 tokens per workgroup
+    ("Float16", 1, 320, 64, 16, [(40, 40), (90, 7)]),     # group 320 as 2 x 160 passes
 ]
 
 
@@ -462,9 +464,10 @@ EXACT_CASES = [  # name, kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     ("Float16", 2, 8, 128, 16, 700, 37),
     ("BFloat16", 1, 8, 128, 32, 333, 333),
     ("Float16", 2, 4, 64, 16, 600, 600),
-    ("BFloat16", 2, 6, 128, 16, 500, 500),      # group 6 (two idle blocks of eight)
-    ("BFloat16", 2, 32, 128, 16, 260, 260),     # group 16 as 2 x 8
-    ("Float16", 1, 12, 64, 64, 333, 333),       # group 12 as 2 x 6
+    ("BFloat16", 2, 6, 128, 16, 500, 500),      # group 6 (two idle rows of 128)
+    ("BFloat16", 2, 32, 128, 16, 260, 260),     # group 16: 8 tokens per workgroup
+    ("Float16", 1, 12, 64, 64, 333, 333),       # group 12 (eight idle rows)
+    ("BFloat16", 1, 200, 64, 16, 50, 20),       # group 200 as 2 x 100 passes
     ("BFloat16", 1, 4, 64, 1, 3000, 300),       # one-token pages
     ("BFloat16", 2, 8, 128, 128, 1000, 1000),   # pages longer than a tile
     ("BFloat16", 8, 32, 128, 16, 8192, 64),     # chunked prefill: keys split over workgroups
@@ -514,9 +517,10 @@ F32_CASES = [  # kv_heads, q_heads, head_size, bs, kv_len, q_tokens
     (2, 8, 128, 16, 1000, 1000),
     (2, 8, 128, 16, 700, 37),
     (1, 4, 64, 16, 600, 600),
-    (2, 6, 128, 32, 500, 500),      # group 6 (two idle blocks of eight)
-    (2, 32, 128, 16, 260, 260),     # group 16 as 2 x 8
-    (1, 12, 64, 64, 333, 333),      # group 12 as 2 x 6
+    (2, 6, 128, 32, 500, 500),      # group 6 (two idle rows of 128)
+    (2, 32, 128, 16, 260, 260),     # group 16: 8 tokens per workgroup
+    (1, 12, 64, 64, 333, 333),      # group 12 (eight idle rows)
+    (1, 136, 64, 16, 60, 17),       # group 136 as 2 x 68 passes
     (1, 4, 64, 1, 3000, 300),       # one-token pages
     (2, 8, 128, 128, 1000, 1000),   # pages longer than a tile
     (1, 2, 128, 2, 40, 40),         # two-token pages, one partial tile
