@@ -737,7 +737,7 @@ def bench_prefill(v2, args, stream):
     del seqs
     tflops = flops / (ms * 1e-3) / 1e12
     return {"workload": "8 x 4096-token causal prefill, 32 q / 8 kv heads, D=128, BF16 KV, block_size 16",
-            "kernel": "paged_prefill_kernel<bf16,128,4>, one batch launch (kvflux_paged_prefill_batch)",
+            "kernel": "paged_prefill_kernel<bf16,128> (group 4), one batch launch (kvflux_paged_prefill_batch)",
             "ms": ms, "ms_one_launch_per_sequence": per_seq_ms, "api_ms": api_ms, "TFLOPs": tflops,
             "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS, "flops": flops,
             # Counter-derived: busy cycles at the clock the part ran (about
@@ -752,7 +752,7 @@ def bench_prefill(v2, args, stream):
                       "max_abs_err_vs_oracle": err_exact, "tolerance": 1e-5},
             # FP32 caches (the same values): one batch launch on
             # v_mfma_f32_16x16x4_f32, against the FP32 MFMA peak.
-            "f32": {"kernel": "paged_prefill_kernel<f32,128,4>, one batch launch", "ms": f32_ms,
+            "f32": {"kernel": "paged_prefill_kernel<f32,128> (group 4), one batch launch", "ms": f32_ms,
                     "TFLOPs": flops / (f32_ms * 1e-3) / 1e12,
                     "frac_of_fp32_mfma_peak": flops / (f32_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
                     "max_abs_err_vs_oracle": err_f32, "tolerance": 1e-5},
