@@ -1526,14 +1526,14 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             // kD = 128 takes 251 VGPRs (no spills, two workgroups per CU):
             // 1.27 against 3.10 ms on the VALU split kernel for 128 rows of
             // U[1024, 32768] tokens with 64 query / 8 kv heads.
+            // Small pages at head_size 128 take sub-groups up to 5 (the
+            // per-lane page addresses of larger ones exceed the registers).
             const auto g = static_cast<std::uint32_t>(group);
-            std::uint32_t sub = g < 8 ? g : 8;
+            const std::uint32_t cap = small && kD == 128 ? kSmallMaxGroup128 : 8u;
+            std::uint32_t sub = g < cap ? g : cap;
             while (g % sub != 0) --sub;
             const std::uint64_t sets = g / sub;  // head sets per kv head, each its own work items
             if (2 * rows * max_chunks * p.heads * sets > 0xffffffffULL) return plan_fallback(group, max_chunks, plan);
-            // Small pages at head_size 128 take groups up to 5 (the per-lane
-            // page addresses of larger groups exceed the registers).
-            if (small && kD == 128 && sub > kSmallMaxGroup128) return plan_fallback(group, max_chunks, plan);
             int slots = 0;
             int status = KVFLUX_OK;
             if constexpr (std::is_same<E, F32>::value && kD == 128) {

@@ -354,7 +354,9 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
     ("Float16", 2, 64, 2, 16),
     ("BFloat16", 4, 128, 1, 5),
     ("Float16", 8, 64, 1, 8),
-    ("BFloat16", 8, 128, 1, 6),   # group 6 at head_size 128: small pages stay on the split kernel
+    ("BFloat16", 8, 128, 1, 6),   # group 6 at head_size 128, small pages: two head sets of 3
+    ("Float16", 4, 128, 1, 7),    # group 7 at head_size 128, small pages: seven head sets of 1
+    ("BFloat16", 2, 128, 2, 16),  # group 8 at head_size 128, small pages: two head sets of 4
     ("BFloat16", 4, 64, 4, 28),   # group 7 at head_size 64 on the small-page kernel
     ("Float32", 32, 128, 2, 8),
     ("Float32", 64, 64, 2, 12),
@@ -371,9 +373,9 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     """Pages of 32, 64 and 128 tokens run on the block-size-16 kernel as
     16-token tiles (a contiguous part of one kv head's rows of a page);
     pages of 1, 2, 4 and 8 tokens too, each 16-token tile gathering its rows
-    from 16 / block_size pages (groups above 5 at head_size 128, and FP32
-    at head_size 128, stay on the split kernel). Lengths sit on tile and page
-    boundaries; table entries
+    from 16 / block_size pages (at head_size 128 a group above 5 runs as
+    head sets of at most 5 heads; FP32 at head_size 128 stays on the split
+    kernel). Lengths sit on tile and page boundaries; table entries
     past a row's pages are poisoned, so a tile's last pages can be missing.
     Matches the oracle at 1e-5, bit-identical on repeat."""
     lib = capi.lib()
