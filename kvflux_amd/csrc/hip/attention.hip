@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attention_split_kernel(Para
     }
 
     // Q slice of every head of the group, pre-scaled into the log2 domain.
-    const std::uint32_t qh0 = kvh * kG;
+    const std::uint32_t qh0 = kvh * p.q_group + p.q_first;  // the heads of this launch
     float q[kG][kDpl];
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
@@ -1448,7 +1448,7 @@ enum class Family { Bs16, Split, Generic };
 
 struct Plan {
     Family family = Family::Generic;
-    std::uint32_t sub = 0;     // Bs16: query heads per launch (divides the group, <= 8)
+    std::uint32_t sub = 0;     // Bs16: heads per item; Split: heads per launch (divides the group)
     bool small = false;        // Bs16: pages of 1 to 8 tokens
     std::uint32_t shift = 9;   // Bs16: log2(tokens per work item)
     unsigned grid = 0;         // Bs16: persistent grid
@@ -1492,10 +1492,14 @@ inline std::uint32_t max_item_shift(std::uint32_t bs) { return bs >= 16 ? 12u : 
 
 constexpr std::uint32_t kSmallMaxGroup128 = 5;
 
-// The VALU kernels: split (groups 1, 2, 4, 8) or generic.
-inline int plan_fallback(std::uint64_t group, std::uint64_t max_chunks, Plan* plan) {
-    if (group == 1 || group == 2 || group == 4 || group == 8) {
+// The VALU kernels: split at head_size 64/128/256, as launches of the
+// largest power of two up to 8 (4 at 256) dividing the group, or generic.
+inline int plan_fallback(std::uint64_t head_dim, std::uint64_t group, std::uint64_t max_chunks, Plan* plan) {
+    if (head_dim == 64 || head_dim == 128 || head_dim == 256) {
+        std::uint64_t sub = head_dim == 256 ? 4 : 8;
+        while (group % sub != 0) sub /= 2;
         plan->family = Family::Split;
+        plan->sub = static_cast<std::uint32_t>(sub);
         plan->chunks = max_chunks;
     } else {
         plan->family = Family::Generic;
@@ -1533,13 +1537,13 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             std::uint32_t sub = g < cap ? g : cap;
             while (g % sub != 0) --sub;
             const std::uint64_t sets = g / sub;  // head sets per kv head, each its own work items
-            if (2 * rows * max_chunks * p.heads * sets > 0xffffffffULL) return plan_fallback(group, max_chunks, plan);
+            if (2 * rows * max_chunks * p.heads * sets > 0xffffffffULL) return plan_fallback(kD, group, max_chunks, plan);
             int slots = 0;
             int status = KVFLUX_OK;
             if constexpr (std::is_same<E, F32>::value && kD == 128) {
                 // FP32 at head_size 128: pages of 16 tokens or more (with small
                 // pages' per-lane page addresses it would spill).
-                if (small) return plan_fallback(group, max_chunks, plan);
+                if (small) return plan_fallback(kD, group, max_chunks, plan);
                 status = resident_slots_for<E, kD, false>(sub, &slots);
             } else {
                 status = small ? resident_slots_for<E, kD, true>(sub, &slots) : resident_slots_for<E, kD, false>(sub, &slots);
@@ -1566,7 +1570,7 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             return KVFLUX_OK;
         }
     }
-    return plan_fallback(group, max_chunks, plan);
+    return plan_fallback(kD, group, max_chunks, plan);
 }
 
 template <typename E>
@@ -1575,9 +1579,7 @@ int plan_call(const Params& p, std::uint64_t rows, std::uint64_t head_dim, std::
     switch (head_dim) {
     case 64: return plan_group<E, 64>(p, rows, group, max_chunks, plan);
     case 128: return plan_group<E, 128>(p, rows, group, max_chunks, plan);
-    case 256:
-        if (group <= 4) return plan_group<E, 256>(p, rows, group, max_chunks, plan);
-        break;
+    case 256: return plan_group<E, 256>(p, rows, group, max_chunks, plan);
     default: break;
     }
     plan->family = Family::Generic;
@@ -1599,21 +1601,43 @@ int launch_combine(Params p, std::uint32_t head_dim, std::uint32_t chunk_tokens,
 }
 
 template <typename E, int kD, int kG>
-int launch_split(Params p, std::uint64_t rows, hipStream_t s) {
+int launch_split_pass(const Params& p, std::uint64_t n, hipStream_t s) {
+    hipLaunchKernelGGL((paged_attention_split_kernel<E, kD, kG>),
+                       dim3(p.max_chunks > 0 ? p.max_chunks : 1u, static_cast<unsigned>(n * p.heads)),
+                       dim3(kThreads), 0, s, p);
+    return launch_status("paged_attention_split_kernel");
+}
+
+// The split kernel over every row: one launch per `sub` query heads of each
+// kv head (sub divides the group), then one combine over all heads.
+template <typename E, int kD>
+int run_split(Params p, std::uint64_t rows, std::uint32_t sub, hipStream_t s) {
     const std::uint64_t rows_per_launch = 65535 / p.heads;
     for (std::uint64_t base = 0; base < rows; base += rows_per_launch) {
         const std::uint64_t n = rows - base < rows_per_launch ? rows - base : rows_per_launch;
         p.row_base = static_cast<std::uint32_t>(base);
-        hipLaunchKernelGGL((paged_attention_split_kernel<E, kD, kG>),
-                           dim3(p.max_chunks > 0 ? p.max_chunks : 1u, static_cast<unsigned>(n * p.heads)),
-                           dim3(kThreads), 0, s, p);
-        int status = launch_status("paged_attention_split_kernel");
-        if (status != KVFLUX_OK) return status;
+        for (std::uint32_t first = 0; first < p.q_group; first += sub) {
+            p.q_first = first;
+            int status = KVFLUX_OK;
+            switch (sub) {
+            case 1: status = launch_split_pass<E, kD, 1>(p, n, s); break;
+            case 2: status = launch_split_pass<E, kD, 2>(p, n, s); break;
+            case 4: status = launch_split_pass<E, kD, 4>(p, n, s); break;
+            default:
+                if constexpr (kD != 256) {
+                    status = launch_split_pass<E, kD, 8>(p, n, s);
+                } else {
+                    status = fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: split sub-group %u", sub);
+                }
+                break;
+            }
+            if (status != KVFLUX_OK) return status;
+        }
         if (p.max_chunks > 1) {
             hipLaunchKernelGGL(paged_attention_combine_kernel,
                                dim3(static_cast<unsigned>(n * p.query_heads)), dim3(kCombineThreads), 0, s,
                                p, static_cast<std::uint32_t>(kD), static_cast<std::uint32_t>(kChunk));
-            status = launch_status("paged_attention_combine_kernel");
+            const int status = launch_status("paged_attention_combine_kernel");
             if (status != KVFLUX_OK) return status;
         }
     }
@@ -1679,15 +1703,6 @@ int run_bs16(Params p, const Plan& plan, hipStream_t s) {
     return KVFLUX_OK;
 }
 
-template <typename E, int kD>
-int run_split(Params p, std::uint64_t rows, std::uint64_t group, hipStream_t s) {
-    switch (group) {
-    case 1: return launch_split<E, kD, 1>(p, rows, s);
-    case 2: return launch_split<E, kD, 2>(p, rows, s);
-    case 4: return launch_split<E, kD, 4>(p, rows, s);
-    default: return launch_split<E, kD, 8>(p, rows, s);
-    }
-}
 
 template <typename E>
 int run_plan(Params p, const Plan& plan, std::uint64_t rows, std::uint64_t head_dim, std::uint64_t group,
@@ -1697,21 +1712,18 @@ int run_plan(Params p, const Plan& plan, std::uint64_t rows, std::uint64_t head_
         if (head_dim == 64) return run_bs16<E, 64>(p, plan, s);
         return run_bs16<E, 128>(p, plan, s);
     case Family::Split:
-        if (head_dim == 64) return run_split<E, 64>(p, rows, group, s);
-        if (head_dim == 128) return run_split<E, 128>(p, rows, group, s);
-        return run_split<E, 256>(p, rows, group, s);
+        if (head_dim == 64) return run_split<E, 64>(p, rows, plan.sub, s);
+        if (head_dim == 128) return run_split<E, 128>(p, rows, plan.sub, s);
+        return run_split<E, 256>(p, rows, plan.sub, s);
     case Family::Generic: break;
     }
     return launch_generic<E>(p, rows, head_dim, s);
 }
 
 // Whether a call may write chunk partials (and so needs the workspace): the
-// block-size-16 kernel at head_size 64/128 with any group, and the split
-// kernel at head_size 64/128 (groups 1, 2, 4, 8) or 256 (groups 1, 2, 4).
+// block-size-16 and split kernels at head_size 64/128/256, any group.
 bool uses_split(std::uint64_t head_dim, std::uint64_t group) {
-    if (head_dim == 64 || head_dim == 128) return group >= 1;
-    if (head_dim == 256) return group == 1 || group == 2 || group == 4;
-    return false;
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && group >= 1;
 }
 
 // Bytes of the partial arrays for `chunks` slots per (row, query head):
