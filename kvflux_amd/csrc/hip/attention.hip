@@ -522,7 +522,9 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 
 // ---------------------------------------------------------------- block_size 16 decode
 // Hot path for head_size 64/128: 16-bit caches with pages of 1 to 128 tokens,
-// FP32 caches with pages of 16 to 128 tokens (1 to 128 at head_size 64):
+// FP32 caches with pages of 16 to 128 tokens (1 to 128 at head_size 64); and
+// head_size 256 with 16-bit caches and pages of 16 to 128 tokens (one
+// workgroup per CU, up to 5 heads per item):
 //  * persistent workgroups walk a plan of (row, chunk, kv head) items built
 //    in LDS from the row lengths (exclusive prefix of chunk counts), so no
 //    workgroup is launched for an empty chunk and consecutive items read the
@@ -607,7 +609,7 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 // token row from the lane holding it (a cross-lane read), where whole tiles
 // take one wave-uniform page.
 template <typename E, int kD, int kG, bool kSmall>
-__global__ __launch_bounds__(kThreads, 2) void paged_decode_bs16_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, kD == 256 ? 1 : 2) void paged_decode_bs16_kernel(Params p) {
     // FP32 caches: QK^T and P*V on v_mfma_f32_16x16x4_f32 with FP32 K, V, Q
     // and weights as they are (no splits, no LDS staging of V).
     constexpr bool kF32 = std::is_same<E, F32>::value;
@@ -1465,8 +1467,8 @@ int resident_slots_for(std::uint32_t sub, int* out) {
     case 5: return resident_slots<E, kD, 5, kSmall>(out);
     default: break;
     }
-    if constexpr (kSmall && kD == 128) {
-        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %u", sub);
+    if constexpr ((kSmall && kD == 128) || kD == 256) {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: a sub-group of %u", sub);
     } else {
         switch (sub) {
         case 6: return resident_slots<E, kD, 6, kSmall>(out);
@@ -1512,7 +1514,7 @@ inline int plan_fallback(std::uint64_t head_dim, std::uint64_t group, std::uint6
 template <typename E, int kD>
 int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::uint64_t max_chunks,
                Plan* plan) {
-    if constexpr (kD == 64 || kD == 128) {
+    if constexpr (kD == 64 || kD == 128 || (kD == 256 && !std::is_same<E, F32>::value)) {
         // The kernel counts work items in 32 bits (at most 512-token chunks);
         // rows <= kPlanRows keeps the product below 2^51.
         const std::uint32_t bs = p.block_size.divisor;
@@ -1532,8 +1534,11 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             // U[1024, 32768] tokens with 64 query / 8 kv heads.
             // Small pages at head_size 128 take sub-groups up to 5 (the
             // per-lane page addresses of larger ones exceed the registers).
+            // Head size 256 (one workgroup per CU, pages of 16 tokens or more)
+            // takes sub-groups up to 5 as well.
+            if (kD == 256 && small) return plan_fallback(kD, group, max_chunks, plan);
             const auto g = static_cast<std::uint32_t>(group);
-            const std::uint32_t cap = small && kD == 128 ? kSmallMaxGroup128 : 8u;
+            const std::uint32_t cap = (small && kD == 128) || kD == 256 ? kSmallMaxGroup128 : 8u;
             std::uint32_t sub = g < cap ? g : cap;
             while (g % sub != 0) --sub;
             const std::uint64_t sets = g / sub;  // head sets per kv head, each its own work items
@@ -1544,6 +1549,8 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
                 // FP32 at head_size 128: pages of 16 tokens or more (with small
                 // pages' per-lane page addresses it would spill).
                 if (small) return plan_fallback(kD, group, max_chunks, plan);
+                status = resident_slots_for<E, kD, false>(sub, &slots);
+            } else if constexpr (kD == 256) {
                 status = resident_slots_for<E, kD, false>(sub, &slots);
             } else {
                 status = small ? resident_slots_for<E, kD, true>(sub, &slots) : resident_slots_for<E, kD, false>(sub, &slots);
@@ -1665,13 +1672,15 @@ int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
     if (plan.small) {
         if constexpr (std::is_same<E, F32>::value && kD == 128) {
             return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: FP32 caches at head_size 128 with pages under 16 tokens");
-        } else if constexpr (kD != 128 || kG <= static_cast<int>(kSmallMaxGroup128)) {
+        } else if constexpr (kD == 64 || (kD == 128 && kG <= static_cast<int>(kSmallMaxGroup128))) {
             hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, true>), dim3(plan.grid), dim3(kThreads), 0, s, p);
         } else {
             return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %d", kG);
         }
-    } else {
+    } else if constexpr (kD != 256 || kG <= static_cast<int>(kSmallMaxGroup128)) {
         hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, false>), dim3(plan.grid), dim3(kThreads), 0, s, p);
+    } else {
+        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: head_size 256 with a group of %d", kG);
     }
     return launch_status("paged_decode_bs16_kernel");
 }
@@ -1710,6 +1719,9 @@ int run_plan(Params p, const Plan& plan, std::uint64_t rows, std::uint64_t head_
     switch (plan.family) {
     case Family::Bs16:
         if (head_dim == 64) return run_bs16<E, 64>(p, plan, s);
+        if constexpr (!std::is_same<E, F32>::value) {
+            if (head_dim == 256) return run_bs16<E, 256>(p, plan, s);
+        }
         return run_bs16<E, 128>(p, plan, s);
     case Family::Split:
         if (head_dim == 64) return run_split<E, 64>(p, rows, plan.sub, s);

@@ -68,6 +68,12 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("Float32", 2, 8, 128, [33, 777]),
     ("BFloat16", 1, 8, 64, [5, 530, 1100]),
     ("BFloat16", 2, 4, 256, [64, 900]),
+    # head_size 256 on the MFMA kernel (one workgroup per CU, up to 5 heads
+    # per item: groups 6 and 8 as two head sets), FP32 on the split kernel
+    ("Float16", 2, 16, 256, [17, 700, 1600]),
+    ("BFloat16", 1, 5, 256, [4, 513, 1200]),
+    ("BFloat16", 2, 12, 256, [9, 600, 1500]),
+    ("Float32", 2, 8, 256, [33, 777]),
     ("Float16", 3, 3, 128, [100, 513]),
     ("BFloat16", 4, 8, 64, [1, 2000]),
     ("BFloat16", 1, 8, 128, [3, 511, 1100, 2049]),
@@ -286,6 +292,7 @@ ITEM_CASES = [  # name, head_size, rows, max_len, query heads (2 kv heads)
     ("BFloat16", 128, 64, 32768, 32),
     ("Float32", 128, 128, 16384, 8),
     ("Float32", 64, 128, 8192, 16),
+    ("BFloat16", 256, 128, 16384, 8),
 ]
 
 
@@ -365,6 +372,7 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
     ("Float32", 4, 64, 1, 5),
     ("Float32", 2, 64, 2, 16),
     ("Float32", 1, 64, 1, 8),
+    ("BFloat16", 8, 256, 2, 8),   # head_size 256 with small pages: split kernel
 ]
 
 
