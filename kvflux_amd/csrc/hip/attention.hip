@@ -521,10 +521,9 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 }
 
 // ---------------------------------------------------------------- block_size 16 decode
-// Hot path for head_size 64/128: 16-bit caches with pages of 1 to 128 tokens,
-// FP32 caches with pages of 16 to 128 tokens (1 to 128 at head_size 64); and
-// head_size 256 with 16-bit caches and pages of 16 to 128 tokens (one
-// workgroup per CU, up to 5 heads per item):
+// Hot path for pages of 1 to 128 tokens: head_size 64/128 with 16-bit and
+// FP32 caches, head_size 256 with 16-bit caches (one workgroup per CU there,
+// and for FP32 small pages at 128; up to 5 heads per item at 256):
 //  * persistent workgroups walk a plan of (row, chunk, kv head) items built
 //    in LDS from the row lengths (exclusive prefix of chunk counts), so no
 //    workgroup is launched for an empty chunk and consecutive items read the
@@ -608,8 +607,15 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 // item size keeps them within 64), and every lane takes the page of its own
 // token row from the lane holding it (a cross-lane read), where whole tiles
 // take one wave-uniform page.
+// One workgroup per CU (the registers of two) at head_size 256 and for FP32
+// tiles gathered from small pages at head_size 128.
+template <typename E, int kD, bool kSmall>
+constexpr int bs16_occupancy() {
+    return kD == 256 || (std::is_same<E, F32>::value && kD == 128 && kSmall) ? 1 : 2;
+}
+
 template <typename E, int kD, int kG, bool kSmall>
-__global__ __launch_bounds__(kThreads, kD == 256 ? 1 : 2) void paged_decode_bs16_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void paged_decode_bs16_kernel(Params p) {
     // FP32 caches: QK^T and P*V on v_mfma_f32_16x16x4_f32 with FP32 K, V, Q
     // and weights as they are (no splits, no LDS staging of V).
     constexpr bool kF32 = std::is_same<E, F32>::value;
@@ -1467,7 +1473,7 @@ int resident_slots_for(std::uint32_t sub, int* out) {
     case 5: return resident_slots<E, kD, 5, kSmall>(out);
     default: break;
     }
-    if constexpr ((kSmall && kD == 128) || kD == 256) {
+    if constexpr ((kSmall && kD == 128 && !std::is_same<E, F32>::value) || kD == 256) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: a sub-group of %u", sub);
     } else {
         switch (sub) {
@@ -1534,27 +1540,19 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             // U[1024, 32768] tokens with 64 query / 8 kv heads.
             // Small pages at head_size 128 take sub-groups up to 5 (the
             // per-lane page addresses of larger ones exceed the registers).
-            // Head size 256 (one workgroup per CU, pages of 16 tokens or more)
-            // takes sub-groups up to 5 as well.
-            if (kD == 256 && small) return plan_fallback(kD, group, max_chunks, plan);
+            // Head size 256 (one workgroup per CU) takes sub-groups up to 5
+            // as well; FP32 tiles need no split columns, so any sub-group up
+            // to 8 fits.
             const auto g = static_cast<std::uint32_t>(group);
-            const std::uint32_t cap = (small && kD == 128) || kD == 256 ? kSmallMaxGroup128 : 8u;
+            constexpr bool kF32Cache = std::is_same<E, F32>::value;
+            const std::uint32_t cap = (small && kD == 128 && !kF32Cache) || kD == 256 ? kSmallMaxGroup128 : 8u;
             std::uint32_t sub = g < cap ? g : cap;
             while (g % sub != 0) --sub;
             const std::uint64_t sets = g / sub;  // head sets per kv head, each its own work items
             if (2 * rows * max_chunks * p.heads * sets > 0xffffffffULL) return plan_fallback(kD, group, max_chunks, plan);
             int slots = 0;
             int status = KVFLUX_OK;
-            if constexpr (std::is_same<E, F32>::value && kD == 128) {
-                // FP32 at head_size 128: pages of 16 tokens or more (with small
-                // pages' per-lane page addresses it would spill).
-                if (small) return plan_fallback(kD, group, max_chunks, plan);
-                status = resident_slots_for<E, kD, false>(sub, &slots);
-            } else if constexpr (kD == 256) {
-                status = resident_slots_for<E, kD, false>(sub, &slots);
-            } else {
-                status = small ? resident_slots_for<E, kD, true>(sub, &slots) : resident_slots_for<E, kD, false>(sub, &slots);
-            }
+            status = small ? resident_slots_for<E, kD, true>(sub, &slots) : resident_slots_for<E, kD, false>(sub, &slots);
             if (status != KVFLUX_OK) return status;
             // Work item size: the largest chunk (up to 4096 tokens, less for
             // small pages) that still gives at least 8 items per resident
@@ -1670,9 +1668,8 @@ template <typename E, int kD, int kG>
 int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
     p.row_base = 0;
     if (plan.small) {
-        if constexpr (std::is_same<E, F32>::value && kD == 128) {
-            return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: FP32 caches at head_size 128 with pages under 16 tokens");
-        } else if constexpr (kD == 64 || (kD == 128 && kG <= static_cast<int>(kSmallMaxGroup128))) {
+        if constexpr (kD == 64 || (kD == 128 && (std::is_same<E, F32>::value || kG <= static_cast<int>(kSmallMaxGroup128))) ||
+                      (kD == 256 && kG <= static_cast<int>(kSmallMaxGroup128))) {
             hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, true>), dim3(plan.grid), dim3(kThreads), 0, s, p);
         } else {
             return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %d", kG);

@@ -367,12 +367,14 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
     ("BFloat16", 4, 64, 4, 28),   # group 7 at head_size 64 on the small-page kernel
     ("Float32", 32, 128, 2, 8),
     ("Float32", 64, 64, 2, 12),
-    ("Float32", 8, 128, 2, 8),    # FP32 at head_size 128 with pages under 16 tokens: split kernel
+    ("Float32", 8, 128, 2, 8),    # FP32 at head_size 128, small pages: one workgroup per CU
+    ("Float32", 2, 128, 1, 6),
     ("Float32", 8, 64, 2, 8),     # FP32 at head_size 64: small pages on the FP32 MFMA kernel
     ("Float32", 4, 64, 1, 5),
     ("Float32", 2, 64, 2, 16),
     ("Float32", 1, 64, 1, 8),
-    ("BFloat16", 8, 256, 2, 8),   # head_size 256 with small pages: split kernel
+    ("BFloat16", 8, 256, 2, 8),   # head_size 256 with small pages
+    ("Float16", 1, 256, 1, 8),    # head_size 256, one-token pages, two head sets of 4
 ]
 
 
@@ -381,9 +383,10 @@ def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
     """Pages of 32, 64 and 128 tokens run on the block-size-16 kernel as
     16-token tiles (a contiguous part of one kv head's rows of a page);
     pages of 1, 2, 4 and 8 tokens too, each 16-token tile gathering its rows
-    from 16 / block_size pages (at head_size 128 a group above 5 runs as
-    head sets of at most 5 heads; FP32 at head_size 128 stays on the split
-    kernel). Lengths sit on tile and page boundaries; table entries
+    from 16 / block_size pages (at head_size 128 with 16-bit caches and at
+    256 a group above 5 runs as head sets of at most 5 heads; FP32 at 128
+    and every cache at 256 run one workgroup per CU). Lengths sit on tile
+    and page boundaries; table entries
     past a row's pages are poisoned, so a tile's last pages can be missing.
     Matches the oracle at 1e-5, bit-identical on repeat."""
     lib = capi.lib()
