@@ -140,7 +140,7 @@ int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
  * Rows longer than one split take two launches: the split kernel and a
  * combine kernel that merges the split partials in ascending split order, so
  * results are deterministic. A split is 512 tokens; the block-size-16 kernel
- * (block_size 1 to 128; head_size 64/128, and 256 with 16-bit caches) uses
+ * (block_size 1 to 256; head_size 64/128, and 256 with 16-bit caches) uses
  * 512 to 4096
  * tokens (pages of bs < 16 tokens: at most 256 * bs, and 256 at bs = 1), the
  * largest that leaves 8 work items per resident workgroup for num_rows rows

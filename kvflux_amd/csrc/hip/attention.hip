@@ -182,7 +182,7 @@ struct Params {
     std::uint32_t q_group;
     std::uint32_t q_first;
     std::uint32_t q_sets;
-    // Block-size-16 kernel: log2(block_size / 16) (pages of 16 to 128
+    // Block-size-16 kernel: log2(block_size / 16) (pages of 16 to 256
     // tokens are cut into 16-token tiles).
     std::uint32_t page_tiles_shift;
     // Block-size-16 kernel on pages of 1 to 8 tokens: log2(16 / block_size)
@@ -521,7 +521,7 @@ __device__ inline float row_shl(float x) {  // lane i <- lane i+kShift within a 
 }
 
 // ---------------------------------------------------------------- block_size 16 decode
-// Hot path for pages of 1 to 128 tokens: head_size 64/128 with 16-bit and
+// Hot path for pages of 1 to 256 tokens: head_size 64/128 with 16-bit and
 // FP32 caches, head_size 256 with 16-bit caches (one workgroup per CU there,
 // and for FP32 small pages at 128; up to 5 heads per item at 256):
 //  * persistent workgroups walk a plan of (row, chunk, kv head) items built
@@ -1526,7 +1526,7 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
         const std::uint32_t bs = p.block_size.divisor;
         const bool small = bs == 1 || bs == 2 || bs == 4 || bs == 8;
         // Items are counted in 32 bits; at most 2 * max_chunks of them.
-        if ((small || bs == 16 || bs == 32 || bs == 64 || bs == 128) && rows <= kPlanRows && p.width > 0 &&
+        if ((small || bs == 16 || bs == 32 || bs == 64 || bs == 128 || bs == 256) && rows <= kPlanRows && p.width > 0 &&
             2 * rows * max_chunks * p.heads <= 0xffffffffULL) {
             // A group above 8 is served as head sets of a sub-group (the
             // largest divisor of the group up to 8), each set a work item of
@@ -1685,7 +1685,7 @@ int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
 template <typename E, int kD>
 int run_bs16(Params p, const Plan& plan, hipStream_t s) {
     const std::uint32_t bs = p.block_size.divisor;
-    p.page_tiles_shift = bs <= 16 ? 0u : bs == 32 ? 1u : bs == 64 ? 2u : 3u;
+    p.page_tiles_shift = bs <= 16 ? 0u : log2_pow2(bs) - 4u;
     p.tile_pages_shift = bs < 16 ? 4u - log2_pow2(bs) : 0u;
     p.bs_shift = log2_pow2(bs);
     p.chunk_shift = plan.shift;

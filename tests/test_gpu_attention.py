@@ -355,6 +355,8 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
     ("BFloat16", 32, 128, 2, 8),
     ("Float16", 64, 64, 2, 16),
     ("BFloat16", 128, 128, 1, 8),
+    ("Float16", 256, 128, 2, 8),     # 256-token pages: sixteen tiles per page
+    ("Float32", 256, 64, 1, 4),
     ("BFloat16", 64, 128, 2, 6),
     ("BFloat16", 8, 128, 2, 8),
     ("BFloat16", 1, 128, 2, 8),
@@ -380,7 +382,7 @@ BS_CASES = [  # name, block_size, head_size, kv heads, query heads
 
 @pytest.mark.parametrize("name,bs,head_size,H,Hq", BS_CASES)
 def test_decode_block_sizes(gpu, name, bs, head_size, H, Hq):
-    """Pages of 32, 64 and 128 tokens run on the block-size-16 kernel as
+    """Pages of 32 to 256 tokens run on the block-size-16 kernel as
     16-token tiles (a contiguous part of one kv head's rows of a page);
     pages of 1, 2, 4 and 8 tokens too, each 16-token tile gathering its rows
     from 16 / block_size pages (at head_size 128 with 16-bit caches and at
