@@ -174,6 +174,7 @@ struct Params {
     float* partial_ml;   // [rows][Hq][max_chunks][2]
     std::uint32_t max_chunks;  // partial slots per (row, query head): ceil(kv_len / kChunk)
     std::uint32_t row_base;  // first row of this launch slice
+    std::uint32_t slice_rows;  // block-size-16 kernel: rows of this launch (at most kPlanRows)
     float scale_log2;        // log2(e) / sqrt(D)
     std::uint32_t chunk_shift;  // block-size-16 kernel: log2(tokens per work item), 9..12
     // Block-size-16 kernel: query heads per kv head (the GQA group), the
@@ -659,7 +660,9 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int col = lane % 16, quad = lane / 16;
-    const std::uint32_t rows = p.num_rows;
+    // This launch's rows: p.row_base + r for r < rows (a batch of more than
+    // kPlanRows rows runs as launches of kPlanRows-row slices).
+    const std::uint32_t rows = p.slice_rows;
 
     // ---- plan: lens[r] = row length (clamped to kv_len), plan[r] = number
     // of chunks of rows < r (a zero-length row still owns one chunk so its
@@ -669,7 +672,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
     for (int i = 0; i < kPer; ++i) {
         const std::uint32_t r = tid * kPer + i;
         if (r < rows) {
-            const std::uint64_t full = row_length(p, r);
+            const std::uint64_t full = row_length(p, p.row_base + r);
             const std::uint32_t len = static_cast<std::uint32_t>(full < p.kv_len ? full : p.kv_len);
             lens[r] = len;
             mine += len == 0 ? 1u : chunks_of(len);
@@ -771,7 +774,8 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
     // wave + kWaves * j, or kNoPage. Small pages: lane j < per_wave << tps
     // holds page slot j (page j & (2^tps - 1) of tile wave + kWaves * (j >> tps)).
     auto fetch_pages = [&](const Item& it) -> std::uint64_t {
-        const std::uint64_t* table_row = p.table + (p.seq_lens ? it.row : 0) * p.width;
+        const std::uint64_t* table_row =
+            p.table + (p.seq_lens ? static_cast<std::uint64_t>(p.row_base) + it.row : 0) * p.width;
         if constexpr (kSmall) {
             const std::uint32_t j = lane & ((per_wave << tps) - 1);
             const std::uint64_t tile = static_cast<std::uint64_t>(it.chunk) * tiles + wave + kWaves * (j >> tps);
@@ -797,7 +801,8 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
     // Query elements tid + kThreads * i of the item's kG heads (clamped).
     auto fetch_query = [&](const Item& it, float (&q)[kQPer]) {
         const float* base =
-            p.query + (static_cast<std::uint64_t>(it.row) * p.query_heads + it.kvh * p.q_group + p.q_first + it.qf) * kD;
+            p.query + ((static_cast<std::uint64_t>(p.row_base) + it.row) * p.query_heads + it.kvh * p.q_group + p.q_first +
+                       it.qf) * kD;
 #pragma unroll
         for (int i = 0; i < kQPer; ++i) {
             const int idx = tid + kThreads * i;
@@ -1243,7 +1248,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
                 l += wstats[w][2 * g + 1] * f;
                 sum += reduce[w * kG * kD + idx] * f;
             }
-            const std::uint64_t out_row = static_cast<std::uint64_t>(cur.row) * p.query_heads + qh0 + g;
+            const std::uint64_t out_row = (static_cast<std::uint64_t>(p.row_base) + cur.row) * p.query_heads + qh0 + g;
             if (single) {
                 p.output[out_row * kD + d] = l > 0.0f ? sum / l : 0.0f;
             } else {
@@ -1526,7 +1531,7 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
         const std::uint32_t bs = p.block_size.divisor;
         const bool small = bs == 1 || bs == 2 || bs == 4 || bs == 8;
         // Items are counted in 32 bits; at most 2 * max_chunks of them.
-        if ((small || bs == 16 || bs == 32 || bs == 64 || bs == 128 || bs == 256) && rows <= kPlanRows && p.width > 0 &&
+        if ((small || bs == 16 || bs == 32 || bs == 64 || bs == 128 || bs == 256) && p.width > 0 &&
             2 * rows * max_chunks * p.heads <= 0xffffffffULL) {
             // A group above 8 is served as head sets of a sub-group (the
             // largest divisor of the group up to 8), each set a work item of
@@ -1665,8 +1670,7 @@ int launch_generic(Params p, std::uint64_t rows, std::uint64_t head_dim, hipStre
 }
 
 template <typename E, int kD, int kG>
-int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
-    p.row_base = 0;
+int launch_bs16_slice(const Params& p, const Plan& plan, hipStream_t s) {
     if (plan.small) {
         if constexpr (kD == 64 || (kD == 128 && (std::is_same<E, F32>::value || kG <= static_cast<int>(kSmallMaxGroup128))) ||
                       (kD == 256 && kG <= static_cast<int>(kSmallMaxGroup128))) {
@@ -1680,6 +1684,18 @@ int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: head_size 256 with a group of %d", kG);
     }
     return launch_status("paged_decode_bs16_kernel");
+}
+
+// A batch of more than kPlanRows rows runs as launches of kPlanRows-row slices.
+template <typename E, int kD, int kG>
+int launch_bs16(Params p, const Plan& plan, hipStream_t s) {
+    for (std::uint64_t base = 0; base < p.num_rows; base += kPlanRows) {
+        p.row_base = static_cast<std::uint32_t>(base);
+        p.slice_rows = static_cast<std::uint32_t>(p.num_rows - base < kPlanRows ? p.num_rows - base : kPlanRows);
+        const int status = launch_bs16_slice<E, kD, kG>(p, plan, s);
+        if (status != KVFLUX_OK) return status;
+    }
+    return KVFLUX_OK;
 }
 
 template <typename E, int kD>
@@ -1796,6 +1812,8 @@ int prepare(const void* key_cache, const void* value_cache, uint64_t num_blocks,
     p->q_group = static_cast<std::uint32_t>(group);
     p->q_first = 0;
     p->q_sets = 1;
+    p->row_base = 0;
+    p->slice_rows = static_cast<std::uint32_t>(num_rows);
     p->scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_size)));
     int status = KVFLUX_OK;
     switch (dtype) {

@@ -531,3 +531,39 @@ def test_decode_random_shapes(gpu, case):
     exp = oracle.paged_attention_rows(kh, vh, H, bs, head_size, code, table.reshape(-1), width, lens, q, Hq,
                                       threads=8)
     assert np.abs(outs[0] - exp).max() < TOL
+
+
+def test_decode_batch_above_plan_rows(gpu):
+    """A decode batch of more than 4096 rows (the rows one launch of the
+    block-size-16 kernel plans in LDS) runs as launches of 4096-row slices:
+    every sampled row, on both sides of the slice boundary, within 1e-5 of
+    the oracle."""
+    lib = capi.lib()
+    name, H, Hq, D, bs, rows, P = "BFloat16", 2, 8, 128, 16, 5000, 4096
+    code, host = DTYPES[name]
+    page = H * bs * D
+    kc, vc = device.DeviceBuffer(P * page * 2), device.DeviceBuffer(P * page * 2)
+    device.fill_random(kc.ptr, P * page, code, 1, 71)
+    device.fill_random(vc.ptr, P * page, code, 1, 72)
+    rng = np.random.default_rng(73)
+    lens = rng.integers(1, 1200, rows).astype(np.uint64)
+    lens[[0, 4095, 4096, 4999]] = [1199, 600, 513, 17]
+    width = (int(lens.max()) + bs - 1) // bs
+    table = rng.integers(0, P, (rows, width)).astype(np.uint64)
+    td, ld = buffer_like(table.reshape(-1)), buffer_like(lens)
+    q = oracle.random_elements(0, rows * Hq * D, oracle.F32, 1, 74)
+    qd = buffer_like(q)
+    ws = C.c_size_t(0)
+    capi.check(lib.kvflux_paged_attention_workspace_size(rows, int(lens.max()), H, Hq, bs, D, C.byref(ws)))
+    wd = device.DeviceBuffer(max(ws.value, 256))
+    od = buffer_like(np.full(q.size, 7.0, np.float32))
+    capi.check(lib.kvflux_paged_attention(kc.ptr, vc.ptr, P, H, bs, D, code, td.ptr, width, ld.ptr, int(lens.max()),
+                                          rows, Hq, qd.ptr, od.ptr, wd.ptr, ws.value, None))
+    device.synchronize()
+    got = od.download(np.float32).reshape(rows, -1)
+    assert np.all(np.isfinite(got))
+    sample = np.array(sorted({0, 1, 4094, 4095, 4096, 4097, 4999} | set(rng.choice(rows, 25, replace=False).tolist())))
+    kh, vh = kc.download(host), vc.download(host)
+    exp = oracle.paged_attention_rows(kh, vh, H, bs, D, code, table[sample].reshape(-1), width, lens[sample],
+                                      q.reshape(rows, -1)[sample].reshape(-1), Hq, threads=8)
+    assert np.abs(got[sample].reshape(-1) - exp).max() < TOL
