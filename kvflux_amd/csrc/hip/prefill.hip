@@ -2,8 +2,9 @@
 // and FP32 caches, head_size 64/128 (v_mfma_f32_16x16x4_f32, see PfF32).
 //
 // One workgroup (8 wavefronts, two per SIMD) owns one kv head and 16 * R rows
-// (R = 16 row blocks of 16; 8 at head_size 256 and in the exact and FP32
-// variants), a row being a (query token, query head) pair of the G query heads
+// (R = 8 * pf_blocks row blocks of 16: 32 at head_size 64, 16 at 128, 8 at
+// 256 and in the exact and FP32 variants), a row being a (query token, query
+// head) pair of the G query heads
 // of that kv head: row r is head r % G of token r / G, so a workgroup takes
 // floor(16 * R / G) tokens of every head and at most G - 1 rows idle (a group
 // above 16 * R runs as passes over sub-groups of heads). Wavefront w owns row
@@ -137,14 +138,16 @@ __device__ inline float max_across_quads(float x) {
 
 constexpr int kPfThreads = 512;   // 8 wavefronts, two per SIMD
 constexpr int kPfWaves = kPfThreads / 64;
-// 16-row blocks per wavefront: two at head_size 64/128, one at 256 (whose
-// accumulators and Q operands take as many registers as two blocks at 128).
-template <int kD>
-constexpr int pf_blocks_per_wave() { return kD == 256 ? 1 : 2; }
-// The same for an element policy: one block in the exact variants (their Q
-// operands take three times the registers).
+// 16-row blocks per wavefront: four at head_size 64, two at 128, one at 256
+// (the accumulators and Q operands of a block grow with the head size; more
+// blocks share each K and V operand read: at 64, four blocks ran 18-22 %
+// faster than two for 8 x 4096 tokens); one in the exact and FP32 variants
+// (three Q parts, or FP32 operands; two at 64 measured no faster).
+inline constexpr int pf_blocks_for(int head_size, bool exact) {
+    return exact ? 1 : head_size == 64 ? 4 : head_size == 256 ? 1 : 2;
+}
 template <typename E, int kD>
-constexpr int pf_blocks() { return E::kExact ? 1 : pf_blocks_per_wave<kD>(); }
+constexpr int pf_blocks() { return pf_blocks_for(kD, E::kExact); }
 constexpr int kPfTileShift = 6;
 constexpr int kPfTile = 1 << kPfTileShift;  // keys per LDS tile
 // Page ids held in LDS per workgroup, one window of the sequence at a time:
@@ -855,7 +858,7 @@ struct PrefillPlan {
 inline PrefillPlan prefill_plan(std::uint64_t head_size, std::uint64_t group, std::uint64_t num_kv_heads,
                                 std::uint64_t kv_len, std::uint64_t query_tokens, std::uint64_t query_heads,
                                 bool exact = false) {
-    const std::uint64_t rows = 16 * (head_size == 256 || exact ? kPfWaves : 2 * kPfWaves);
+    const std::uint64_t rows = 16 * kPfWaves * pf_blocks_for(static_cast<int>(head_size), exact);
     const std::uint64_t sub = prefill_sub_group(static_cast<std::uint32_t>(group), static_cast<std::uint32_t>(rows));
     const std::uint64_t tok = rows / sub;
     const std::uint64_t wgs = (query_tokens + tok - 1) / tok * num_kv_heads;
