@@ -192,9 +192,10 @@ int kvflux_paged_attention_noalloc(const void* key_cache, const void* value_cach
  * 1e-5 contract of kvflux_paged_prefill_exact, head_size 64 or 128).
  * KVFLUX_ERR_UNSUPPORTED unless head_size is 64, 128 or 256 (F32: 64 or
  * 128), block_size is a power of two up to 256 and kv_len is below 2^31.
- * Any GQA group query_heads / num_kv_heads: up to 256 (128 at head_size 256
- * and in the exact and F32 variants) in one launch, a larger group as one
- * launch per sub-group of heads (its largest divisor that one launch takes).
+ * Any GQA group query_heads / num_kv_heads: up to 512 at head_size 64, 256 at
+ * 128 and 128 at 256 and in the exact and F32 variants in one launch, a
+ * larger group as one launch per sub-group of heads (its largest divisor that
+ * one launch takes).
  * ------------------------------------------------------------------------- */
 int kvflux_paged_prefill(const void* key_cache, const void* value_cache,
                          uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
