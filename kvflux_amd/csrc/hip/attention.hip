@@ -614,9 +614,13 @@ template <typename E, int kD, bool kSmall>
 constexpr int bs16_occupancy() {
     return kD == 256 || (std::is_same<E, F32>::value && kD == 128 && kSmall) ? 1 : 2;
 }
+template <typename E, int kD, int kG, bool kSmall>
+constexpr int bs16_occupancy_g() {
+    return kG > 8 && kD == 128 ? 1 : bs16_occupancy<E, kD, kSmall>();
+}
 
 template <typename E, int kD, int kG, bool kSmall>
-__global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void paged_decode_bs16_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) void paged_decode_bs16_kernel(Params p) {
     // FP32 caches: QK^T and P*V on v_mfma_f32_16x16x4_f32 with FP32 K, V, Q
     // and weights as they are (no splits, no LDS staging of V).
     constexpr bool kF32 = std::is_same<E, F32>::value;
@@ -631,7 +635,10 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
     constexpr int kVLoads = kD / 32;        // 16-byte V chunks per lane per tile
     constexpr int kRowStep = 64 / kCpr;     // token rows covered by one wave-wide load
     constexpr int kSwz = kCpr / 8;          // LDS slot swizzle multiplier
-    constexpr int kSets = kF32 || 3 * kG <= 16 ? 1 : 2;
+    // Column sets of the split Q parts: one for G <= 5 (hi, mid, lo of G heads
+    // side by side), two for G = 6..8 (lo in the second), three for G = 9..16
+    // (set s holds part s of every head, column = head).
+    constexpr int kSets = kF32 || 3 * kG <= 16 ? 1 : kG <= 8 ? 2 : 3;
     constexpr int kRowBytes = kD * 2;
     constexpr int kQPer = (kG * kD + kThreads - 1) / kThreads;
     static_assert(kRowStep * kVLoads == kBs, "V tile covers 16 tokens");
@@ -921,7 +928,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
     // consume(): V of the tile into the wave's LDS slot and the QK^T MFMAs;
     // after it the tile's registers are free for the next load.
     struct Scores {
-        f32x4_t s0, s1;
+        f32x4_t s0, s1, s2;  // one per column set (s2: groups 9..16)
         std::uint32_t valid;
     };
     auto consume = [&](std::uint32_t valid, const Tile& b) -> Scores {
@@ -953,11 +960,13 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
             }
             out.s0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             out.s1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            out.s2 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int kk = 0; kk < kSteps; ++kk) {
                 const Vec a = __builtin_bit_cast(Vec, b.k[kk]);
                 out.s0 = M::mma(a, qb[0][kk], out.s0);
-                if constexpr (kSets == 2) out.s1 = M::mma(a, qb[1][kk], out.s1);
+                if constexpr (kSets >= 2) out.s1 = M::mma(a, qb[1][kk], out.s1);
+                if constexpr (kSets == 3) out.s2 = M::mma(a, qb[2][kk], out.s2);
             }
         }
         return out;
@@ -1021,8 +1030,10 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
             for (int r = 0; r < 4; ++r) {
                 if constexpr (kSets == 1) {
                     sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + row_shl<2 * kG>(in.s0[r]);
-                } else {
+                } else if constexpr (kSets == 2) {
                     sc[r] = in.s0[r] + row_shl<kG>(in.s0[r]) + in.s1[r];
+                } else {
+                    sc[r] = (in.s0[r] + in.s1[r]) + in.s2[r];
                 }
                 if (valid < kBs && static_cast<std::uint32_t>(quad * 4 + r) >= valid) sc[r] = -INFINITY;
             }
@@ -1038,7 +1049,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
             // Weights, split into three 16-bit parts and routed to the columns
             // (split, head): lane col < kG keeps hi, the mid and lo parts move kG
             // and 2*kG lanes up the row.
-            std::uint32_t w0[4], w1[4];
+            std::uint32_t w0[4], w1[4], w2[4];
             float psum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -1046,27 +1057,41 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
                 psum += pr;
                 std::uint32_t whi, wmid, wlo;
                 M::split3(pr, whi, wmid, wlo);
-                w0[r] = route<kG, kSets>(whi, wmid, wlo, col);
-                if constexpr (kSets == 2) w1[r] = wlo;
+                if constexpr (kSets == 3) {
+                    w0[r] = whi;
+                    w1[r] = wmid;
+                    w2[r] = wlo;
+                } else {
+                    w0[r] = route<kG, kSets>(whi, wmid, wlo, col);
+                    if constexpr (kSets == 2) w1[r] = wlo;
+                }
             }
             run_sum = run_sum * alpha + psum;
 
             // Rescale the columns whose reference point moved (never needed while
             // nothing has been accumulated yet).
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(col < kG && grow && old_max != -INFINITY) != 0, 0)) {
-                const float a0 = __uint_as_float(route<kG, kSets>(__float_as_uint(alpha), __float_as_uint(alpha),
-                                                                  __float_as_uint(alpha), col));
+                if constexpr (kSets == 3) {
 #pragma unroll
-                for (int dt = 0; dt < kDt; ++dt) acc[0][dt] *= a0;
-                if constexpr (kSets == 2) {
+                    for (int m = 0; m < 3; ++m)
 #pragma unroll
-                    for (int dt = 0; dt < kDt; ++dt) acc[1][dt] *= alpha;
+                        for (int dt = 0; dt < kDt; ++dt) acc[m][dt] *= alpha;
+                } else {
+                    const float a0 = __uint_as_float(route<kG, kSets>(__float_as_uint(alpha), __float_as_uint(alpha),
+                                                                      __float_as_uint(alpha), col));
+#pragma unroll
+                    for (int dt = 0; dt < kDt; ++dt) acc[0][dt] *= a0;
+                    if constexpr (kSets == 2) {
+#pragma unroll
+                        for (int dt = 0; dt < kDt; ++dt) acc[1][dt] *= alpha;
+                    }
                 }
             }
 
             const i16x4_t pb0 = M::pack(w0);
-            i16x4_t pb1;
-            if constexpr (kSets == 2) pb1 = M::pack(w1);
+            i16x4_t pb1, pb2;
+            if constexpr (kSets >= 2) pb1 = M::pack(w1);
+            if constexpr (kSets == 3) pb2 = M::pack(w2);
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) {
                 lds_i16x4_t* src = (lds_i16x4_t*)((__attribute__((address_space(3))) char*)(
@@ -1074,7 +1099,8 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
                                        (v_read ^ (dt << 5)));
                 const i16x4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(src);
                 acc[0][dt] = M::mma16(va, pb0, acc[0][dt]);
-                if constexpr (kSets == 2) acc[1][dt] = M::mma16(va, pb1, acc[1][dt]);
+                if constexpr (kSets >= 2) acc[1][dt] = M::mma16(va, pb1, acc[1][dt]);
+                if constexpr (kSets == 3) acc[2][dt] = M::mma16(va, pb2, acc[2][dt]);
             }
         }
     };
@@ -1128,6 +1154,10 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
         for (int m = 0; m < kSets; ++m) {
             int split = col / kG, g = col % kG;
             if (kSets == 2 && m == 1) split = 2;
+            if (kSets == 3) {
+                split = m;  // set m: part m of head col (columns past the group read head 0)
+                g = col < kG ? col : 0;
+            }
             if (split > 2) split = 2;
 #pragma unroll
             for (int kk = 0; kk < kSteps; ++kk) {
@@ -1220,8 +1250,10 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy<E, kD, kSmall>())) void p
                     const float x = acc[0][dt][r];
                     if constexpr (kSets == 1) {
                         op[r] = x + row_shl<kG>(x) + row_shl<2 * kG>(x);
-                    } else {
+                    } else if constexpr (kSets == 2) {
                         op[r] = x + row_shl<kG>(x) + acc[1][dt][r];
+                    } else {
+                        op[r] = (x + acc[1][dt][r]) + acc[2][dt][r];
                     }
                 }
                 if (col < kG) *reinterpret_cast<float4*>(reduce + (wave * kG + col) * kD + dt * 16 + quad * 4) = o;
@@ -1484,8 +1516,18 @@ int resident_slots_for(std::uint32_t sub, int* out) {
         switch (sub) {
         case 6: return resident_slots<E, kD, 6, kSmall>(out);
         case 7: return resident_slots<E, kD, 7, kSmall>(out);
-        default: return resident_slots<E, kD, 8, kSmall>(out);
+        case 8: return resident_slots<E, kD, 8, kSmall>(out);
+        default: break;
         }
+        if constexpr (!kSmall && !std::is_same<E, F32>::value) {
+            switch (sub) {
+            case 10: return resident_slots<E, kD, 10, kSmall>(out);
+            case 12: return resident_slots<E, kD, 12, kSmall>(out);
+            case 16: return resident_slots<E, kD, 16, kSmall>(out);
+            default: break;
+            }
+        }
+        return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: a sub-group of %u", sub);
     }
 }
 
@@ -1553,6 +1595,18 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             const std::uint32_t cap = (small && kD == 128 && !kF32Cache) || kD == 256 ? kSmallMaxGroup128 : 8u;
             std::uint32_t sub = g < cap ? g : cap;
             while (g % sub != 0) --sub;
+            // 16-bit caches with pages of 16 tokens or more at head_size 64/128
+            // also take items of 10, 12 or 16 heads (three column sets; one
+            // workgroup per CU at 128), so groups 10, 12 and 16 (and their
+            // multiples) read each page once.
+            if (!kF32Cache && !small && kD != 256 && g > 8) {
+                for (const std::uint32_t wide : {16u, 12u, 10u}) {
+                    if (g % wide == 0) {
+                        sub = wide;
+                        break;
+                    }
+                }
+            }
             const std::uint64_t sets = g / sub;  // head sets per kv head, each its own work items
             if (2 * rows * max_chunks * p.heads * sets > 0xffffffffULL) return plan_fallback(kD, group, max_chunks, plan);
             int slots = 0;
@@ -1672,13 +1726,15 @@ int launch_generic(Params p, std::uint64_t rows, std::uint64_t head_dim, hipStre
 template <typename E, int kD, int kG>
 int launch_bs16_slice(const Params& p, const Plan& plan, hipStream_t s) {
     if (plan.small) {
-        if constexpr (kD == 64 || (kD == 128 && (std::is_same<E, F32>::value || kG <= static_cast<int>(kSmallMaxGroup128))) ||
-                      (kD == 256 && kG <= static_cast<int>(kSmallMaxGroup128))) {
+        if constexpr (kG <= 8 &&
+                      (kD == 64 || (kD == 128 && (std::is_same<E, F32>::value || kG <= static_cast<int>(kSmallMaxGroup128))) ||
+                       (kD == 256 && kG <= static_cast<int>(kSmallMaxGroup128)))) {
             hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, true>), dim3(plan.grid), dim3(kThreads), 0, s, p);
         } else {
             return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %d", kG);
         }
-    } else if constexpr (kD != 256 || kG <= static_cast<int>(kSmallMaxGroup128)) {
+    } else if constexpr ((kD != 256 || kG <= static_cast<int>(kSmallMaxGroup128)) &&
+                         (kG <= 8 || !std::is_same<E, F32>::value)) {
         hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, false>), dim3(plan.grid), dim3(kThreads), 0, s, p);
     } else {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: head_size 256 with a group of %d", kG);
@@ -1718,7 +1774,10 @@ int run_bs16(Params p, const Plan& plan, hipStream_t s) {
     case 5: status = launch_bs16<E, kD, 5>(p, plan, s); break;
     case 6: status = launch_bs16<E, kD, 6>(p, plan, s); break;
     case 7: status = launch_bs16<E, kD, 7>(p, plan, s); break;
-    default: status = launch_bs16<E, kD, 8>(p, plan, s); break;
+    case 8: status = launch_bs16<E, kD, 8>(p, plan, s); break;
+    case 10: status = launch_bs16<E, kD, 10>(p, plan, s); break;
+    case 12: status = launch_bs16<E, kD, 12>(p, plan, s); break;
+    default: status = launch_bs16<E, kD, 16>(p, plan, s); break;
     }
     if (status != KVFLUX_OK) return status;
     if (p.max_chunks > 1) return launch_combine(p, kD, 1u << plan.shift, s);

@@ -84,6 +84,11 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("Float16", 1, 7, 128, [2, 777, 2100]),
     ("BFloat16", 4, 28, 128, [100, 1300]),
     ("BFloat16", 2, 32, 128, [15, 640, 1700]),
+    # items of 10, 12 and 16 heads (three column sets): groups 10, 12, 16, 32
+    ("Float16", 1, 10, 128, [3, 700, 2100]),
+    ("BFloat16", 2, 24, 128, [17, 513, 1500]),
+    ("BFloat16", 1, 16, 64, [1, 600, 1111]),
+    ("Float16", 1, 32, 128, [40, 1024, 1800]),
     ("Float16", 1, 12, 64, [5, 1030]),
     ("BFloat16", 2, 20, 128, [300, 1111]),
     ("BFloat16", 1, 11, 64, [1, 900]),
