@@ -40,7 +40,7 @@ def decode_case(rng, i):
     name = ("BFloat16", "Float16", "Float32")[int(rng.integers(3))]
     D = int(rng.choice([16, 32, 64, 80, 96, 128, 160, 256, 512]))
     H = int(rng.choice([1, 2, 4, 8]))
-    Hq = H * int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 12, 16]))
+    Hq = H * int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 16, 24]))
     bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64, 128, 256]))
     rows = int(rng.integers(1, 33))
     lens = rng.integers(1, int(rng.choice([64, 600, 5000, 20000])) + 1, rows).astype(np.uint64)
