@@ -616,7 +616,7 @@ constexpr int bs16_occupancy() {
 }
 template <typename E, int kD, int kG, bool kSmall>
 constexpr int bs16_occupancy_g() {
-    return kG > 8 && kD == 128 ? 1 : bs16_occupancy<E, kD, kSmall>();
+    return kG > 8 && kD == 128 && !std::is_same<E, F32>::value ? 1 : bs16_occupancy<E, kD, kSmall>();
 }
 
 template <typename E, int kD, int kG, bool kSmall>
@@ -1519,7 +1519,7 @@ int resident_slots_for(std::uint32_t sub, int* out) {
         case 8: return resident_slots<E, kD, 8, kSmall>(out);
         default: break;
         }
-        if constexpr (!kSmall && !std::is_same<E, F32>::value) {
+        if constexpr (!kSmall) {
             switch (sub) {
             case 10: return resident_slots<E, kD, 10, kSmall>(out);
             case 12: return resident_slots<E, kD, 12, kSmall>(out);
@@ -1595,11 +1595,11 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             const std::uint32_t cap = (small && kD == 128 && !kF32Cache) || kD == 256 ? kSmallMaxGroup128 : 8u;
             std::uint32_t sub = g < cap ? g : cap;
             while (g % sub != 0) --sub;
-            // 16-bit caches with pages of 16 tokens or more at head_size 64/128
-            // also take items of 10, 12 or 16 heads (three column sets; one
+            // Pages of 16 tokens or more at head_size 64/128 also take items
+            // of 10, 12 or 16 heads (16-bit caches: three column sets; one
             // workgroup per CU at 128), so groups 10, 12 and 16 (and their
             // multiples) read each page once.
-            if (!kF32Cache && !small && kD != 256 && g > 8) {
+            if (!small && kD != 256 && g > 8) {
                 for (const std::uint32_t wide : {16u, 12u, 10u}) {
                     if (g % wide == 0) {
                         sub = wide;
@@ -1733,8 +1733,7 @@ int launch_bs16_slice(const Params& p, const Plan& plan, hipStream_t s) {
         } else {
             return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: small pages with a group of %d", kG);
         }
-    } else if constexpr ((kD != 256 || kG <= static_cast<int>(kSmallMaxGroup128)) &&
-                         (kG <= 8 || !std::is_same<E, F32>::value)) {
+    } else if constexpr (kD != 256 || kG <= static_cast<int>(kSmallMaxGroup128)) {
         hipLaunchKernelGGL((paged_decode_bs16_kernel<E, kD, kG, false>), dim3(plan.grid), dim3(kThreads), 0, s, p);
     } else {
         return fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: head_size 256 with a group of %d", kG);
