@@ -752,13 +752,28 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
     auto uniform = [](std::uint32_t x) { return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x))); };
     auto locate = [&](std::uint32_t item) -> Item {
         Item it;
-        it.kvh = uniform(item % p.heads);
-        // Head sets of one (row, chunk, kv head) are p.heads items apart, so
-        // with 8 kv heads they run on one XCD at about the same time and the
-        // later ones find the pages in its L2.
-        const std::uint32_t hs = item / p.heads;
-        it.qf = uniform((hs % p.q_sets) * kG);
-        const std::uint32_t rc = hs / p.q_sets;
+        // Block q = (row/chunk) * heads + kv head. Blocks go in groups of 8,
+        // each group as its head sets one after another (item = group * 8 *
+        // sets + set * 8 + q % 8), so the sets of a block are 8 items apart:
+        // with a persistent grid that is a multiple of 8 they run on one XCD
+        // at about the same time and the later ones find the pages in its L2.
+        // The blocks past the last whole group take the sets in turn. With
+        // one set this is item = q.
+        const std::uint32_t group_items = 8u * p.q_sets;
+        const std::uint32_t whole = (total / group_items) * group_items;
+        std::uint32_t q, set;
+        if (item < whole) {
+            const std::uint32_t in_group = item % group_items;
+            set = in_group / 8u;
+            q = (item / group_items) * 8u + in_group % 8u;
+        } else {
+            const std::uint32_t tail_blocks = (total - whole) / p.q_sets;
+            set = (item - whole) / tail_blocks;
+            q = whole / p.q_sets + (item - whole) % tail_blocks;
+        }
+        it.kvh = uniform(q % p.heads);
+        it.qf = uniform(set * kG);
+        const std::uint32_t rc = q / p.heads;
         if (rc < rows) {
             it.row = uniform(rc);
             it.chunk = 0;
