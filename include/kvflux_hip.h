@@ -140,12 +140,14 @@ int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
  * Rows longer than one split take two launches: the split kernel and a
  * combine kernel that merges the split partials in ascending split order, so
  * results are deterministic. A split is 512 tokens; the block-size-16 kernel
- * (block_size 1 to 256; head_size 64/128, and 256 with 16-bit caches) uses
- * 512 to 4096
- * tokens (pages of bs < 16 tokens: at most 256 * bs, and 256 at bs = 1), the
+ * (power-of-two block_size 1 to 256; head_size 64/128, and 256 with 16-bit
+ * caches; any GQA group, as items of up to 16 heads) uses 512 to 4096 tokens
+ * (pages of bs < 16 tokens: at most 256 * bs, and 256 at bs = 1), the
  * largest that leaves 8 work items per resident workgroup for num_rows rows
  * of kv_len tokens. The workspace is sized for 512-token splits (256 at
- * block_size 1), enough for either.
+ * block_size 1), enough for either. Every num_rows, kv_len and group is
+ * accepted; shapes outside these take the split kernel (head_size 64/128/256)
+ * or a generic kernel (any other head_size up to 512).
  * ------------------------------------------------------------------------- */
 int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t kv_len,
                                           uint64_t num_kv_heads, uint64_t query_heads,
