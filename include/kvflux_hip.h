@@ -145,9 +145,10 @@ int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
  * (pages of bs < 16 tokens: at most 256 * bs, and 256 at bs = 1), the
  * largest that leaves 8 work items per resident workgroup for num_rows rows
  * of kv_len tokens. The workspace is sized for 512-token splits (256 at
- * block_size 1), enough for either. Every num_rows, kv_len and group is
- * accepted; shapes outside these take the split kernel (head_size 64/128/256)
- * or a generic kernel (any other head_size up to 512).
+ * block_size 1), enough for either. Any group is accepted (num_rows and
+ * kv_len below 2^32, at most 65535 kv heads); shapes outside these take the
+ * split kernel (head_size 64/128/256) or a generic kernel (any other
+ * head_size up to 512).
  * ------------------------------------------------------------------------- */
 int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t kv_len,
                                           uint64_t num_kv_heads, uint64_t query_heads,
