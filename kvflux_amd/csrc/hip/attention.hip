@@ -1513,6 +1513,8 @@ struct Plan {
     std::uint32_t shift = 9;   // Bs16: log2(tokens per work item)
     unsigned grid = 0;         // Bs16: persistent grid
     std::uint64_t chunks = 0;  // partial slots per (row, query head); <= 1: no partials
+    std::uint32_t rest = 0;    // Bs16: heads past the last whole set (a second launch), 0 if none
+    unsigned rest_grid = 0;    // Bs16: persistent grid of that launch
 };
 
 template <typename E, int kD, bool kSmall>
@@ -1622,8 +1624,21 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
                     }
                 }
             }
+            // A group whose largest divisor that fits is small (a prime above
+            // 8, say) takes sets of 16 (or 8) heads plus one launch for the
+            // heads past the last set, rather than many narrow sets.
+            std::uint32_t rest = 0;
+            if (!small && kD != 256 && g > 8 && sub < 4) {
+                sub = g > 16 && g % 16 <= 8 ? 16u : 8u;
+                rest = g % sub;
+            }
             const std::uint64_t sets = g / sub;  // head sets per kv head, each its own work items
             if (2 * rows * max_chunks * p.heads * sets > 0xffffffffULL) return plan_fallback(kD, group, max_chunks, plan);
+            int rest_slots = 0;
+            if (rest > 0) {
+                const int st = resident_slots_for<E, kD, false>(rest, &rest_slots);
+                if (st != KVFLUX_OK) return st;
+            }
             int slots = 0;
             int status = KVFLUX_OK;
             status = small ? resident_slots_for<E, kD, true>(sub, &slots) : resident_slots_for<E, kD, false>(sub, &slots);
@@ -1646,6 +1661,10 @@ int plan_group(const Params& p, std::uint64_t rows, std::uint64_t group, std::ui
             plan->shift = shift;
             plan->grid = static_cast<unsigned>(items == 0 ? 1 : items < static_cast<std::uint64_t>(slots) ? items : slots);
             plan->chunks = chunks;
+            plan->rest = rest;
+            const std::uint64_t rest_items = rows * chunks * p.heads;
+            plan->rest_grid = static_cast<unsigned>(
+                rest_items == 0 ? 1 : rest_items < static_cast<std::uint64_t>(rest_slots) ? rest_items : rest_slots);
             return KVFLUX_OK;
         }
     }
@@ -1776,10 +1795,29 @@ int run_bs16(Params p, const Plan& plan, hipStream_t s) {
     p.bs_shift = log2_pow2(bs);
     p.chunk_shift = plan.shift;
     // One launch: a group above 8 is served as head sets of the sub-group,
-    // each a work item of its own.
+    // each a work item of its own (and the heads past the last whole set, if
+    // any, by a second launch).
     p.q_first = 0;
     p.q_sets = p.q_group / plan.sub;
     int status = KVFLUX_OK;
+    if (plan.rest > 0) {
+        Params r = p;
+        r.q_first = plan.sub * p.q_sets;
+        r.q_sets = 1;
+        Plan rp = plan;
+        rp.grid = plan.rest_grid;
+        switch (plan.rest) {
+        case 1: status = launch_bs16<E, kD, 1>(r, rp, s); break;
+        case 2: status = launch_bs16<E, kD, 2>(r, rp, s); break;
+        case 3: status = launch_bs16<E, kD, 3>(r, rp, s); break;
+        case 4: status = launch_bs16<E, kD, 4>(r, rp, s); break;
+        case 5: status = launch_bs16<E, kD, 5>(r, rp, s); break;
+        case 6: status = launch_bs16<E, kD, 6>(r, rp, s); break;
+        case 7: status = launch_bs16<E, kD, 7>(r, rp, s); break;
+        default: status = launch_bs16<E, kD, 8>(r, rp, s); break;
+        }
+        if (status != KVFLUX_OK) return status;
+    }
     switch (plan.sub) {
     case 1: status = launch_bs16<E, kD, 1>(p, plan, s); break;
     case 2: status = launch_bs16<E, kD, 2>(p, plan, s); break;

@@ -89,6 +89,10 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("BFloat16", 2, 24, 128, [17, 513, 1500]),
     ("BFloat16", 1, 16, 64, [1, 600, 1111]),
     ("Float16", 1, 32, 128, [40, 1024, 1800]),
+    # groups whose divisors are small: sets of 8 or 16 heads plus a launch for the rest
+    ("BFloat16", 2, 22, 128, [5, 800, 1700]),    # 11 = 8 + 3
+    ("Float32", 1, 23, 64, [33, 900]),           # 23 = 16 + 7
+    ("Float16", 1, 71, 128, [2, 513, 1300]),     # 71 = 4 x 16 + 7
     ("Float16", 1, 12, 64, [5, 1030]),
     ("BFloat16", 2, 20, 128, [300, 1111]),
     ("BFloat16", 1, 11, 64, [1, 900]),
