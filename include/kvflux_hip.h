@@ -147,7 +147,7 @@ int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
  * of kv_len tokens. The workspace is sized for 512-token splits (256 at
  * block_size 1), enough for either. Any group is accepted (num_rows and
  * kv_len below 2^32, at most 65535 kv heads); shapes outside these take the
- * split kernel (head_size 64/128/256) or a generic kernel (any other
+ * split kernel (head_size 64/80/96/128/256) or a generic kernel (any other
  * head_size up to 512).
  * ------------------------------------------------------------------------- */
 int kvflux_paged_attention_workspace_size(uint64_t num_rows, uint64_t kv_len,

@@ -105,6 +105,8 @@ constexpr int kQuadXor1 = 0xb1;        // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4e;        // quad_perm [2,3,0,1]
 constexpr int kRowHalfMirror = 0x141;  // lane i <- 7-i within 8 lanes
 constexpr int kRowRor8 = 0x128;        // lane i <- (i+8) mod 16 within a row
+constexpr int kRowRor4 = 0x124;        // lane i <- (i+4) mod 16 within a row
+constexpr int kRowRor2 = 0x122;        // lane i <- (i+2) mod 16 within a row
 
 __device__ inline float swizzle_xor16(float x) {
     // ds_swizzle bit mode: and_mask 0x1f, or_mask 0, xor_mask 0x10.
@@ -150,7 +152,10 @@ template <int kD, int kG>
 struct Shape {
     // Elements per lane: 16 keeps Q and the accumulators at 2*G*16 VGPRs;
     // G = 8 uses 8 so the budget stays at 128.
-    static constexpr int kDpl = (kD == 64 || kG >= 8) ? 8 : 16;
+    // Head sizes 96 and 80 (groups of at most 2 and 1 per launch): 24 and 40
+    // elements per lane, whole 16-byte vectors of a row split over 4 and 2
+    // lanes.
+    static constexpr int kDpl = kD == 96 ? 24 : kD == 80 ? 40 : (kD == 64 || kG >= 8) ? 8 : 16;
     static constexpr int kLpt = kD / kDpl;  // lanes per token row
     static constexpr int kTpp = 64 / kLpt;  // tokens per wave pass
     static_assert(kLpt >= 2 && kLpt <= 32 && (kLpt & (kLpt - 1)) == 0, "lane split");
@@ -383,6 +388,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_attention_split_kernel(Para
 #pragma unroll
         for (int i = 0; i < kDpl; ++i) {
             float a = acc[g][i];
+            if constexpr (kLpt <= 2) a += dpp<kRowRor2>(a);
+            if constexpr (kLpt <= 4) a += dpp<kRowRor4>(a);
             if constexpr (kLpt <= 8) a += dpp<kRowRor8>(a);
             if constexpr (kLpt <= 16) a += swizzle_xor16(a);
             acc[g][i] = a;
@@ -1567,8 +1574,8 @@ constexpr std::uint32_t kSmallMaxGroup128 = 5;
 // The VALU kernels: split at head_size 64/128/256, as launches of the
 // largest power of two up to 8 (4 at 256) dividing the group, or generic.
 inline int plan_fallback(std::uint64_t head_dim, std::uint64_t group, std::uint64_t max_chunks, Plan* plan) {
-    if (head_dim == 64 || head_dim == 128 || head_dim == 256) {
-        std::uint64_t sub = head_dim == 256 ? 4 : 8;
+    if (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 96 || head_dim == 80) {
+        std::uint64_t sub = head_dim == 256 ? 4 : head_dim == 96 ? 2 : head_dim == 80 ? 1 : 8;
         while (group % sub != 0) sub /= 2;
         plan->family = Family::Split;
         plan->sub = static_cast<std::uint32_t>(sub);
@@ -1678,6 +1685,8 @@ int plan_call(const Params& p, std::uint64_t rows, std::uint64_t head_dim, std::
     case 64: return plan_group<E, 64>(p, rows, group, max_chunks, plan);
     case 128: return plan_group<E, 128>(p, rows, group, max_chunks, plan);
     case 256: return plan_group<E, 256>(p, rows, group, max_chunks, plan);
+    case 96:
+    case 80: return plan_fallback(head_dim, group, max_chunks, plan);
     default: break;
     }
     plan->family = Family::Generic;
@@ -1717,17 +1726,23 @@ int run_split(Params p, std::uint64_t rows, std::uint32_t sub, hipStream_t s) {
         for (std::uint32_t first = 0; first < p.q_group; first += sub) {
             p.q_first = first;
             int status = KVFLUX_OK;
-            switch (sub) {
-            case 1: status = launch_split_pass<E, kD, 1>(p, n, s); break;
-            case 2: status = launch_split_pass<E, kD, 2>(p, n, s); break;
-            case 4: status = launch_split_pass<E, kD, 4>(p, n, s); break;
-            default:
-                if constexpr (kD != 256) {
-                    status = launch_split_pass<E, kD, 8>(p, n, s);
-                } else {
-                    status = fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: split sub-group %u", sub);
+            if constexpr (kD == 80) {
+                status = launch_split_pass<E, kD, 1>(p, n, s);
+            } else if constexpr (kD == 96) {
+                status = sub == 2 ? launch_split_pass<E, kD, 2>(p, n, s) : launch_split_pass<E, kD, 1>(p, n, s);
+            } else {
+                switch (sub) {
+                case 1: status = launch_split_pass<E, kD, 1>(p, n, s); break;
+                case 2: status = launch_split_pass<E, kD, 2>(p, n, s); break;
+                case 4: status = launch_split_pass<E, kD, 4>(p, n, s); break;
+                default:
+                    if constexpr (kD != 256) {
+                        status = launch_split_pass<E, kD, 8>(p, n, s);
+                    } else {
+                        status = fail(KVFLUX_ERR_UNSUPPORTED, "paged attention: split sub-group %u", sub);
+                    }
+                    break;
                 }
-                break;
             }
             if (status != KVFLUX_OK) return status;
         }
@@ -1850,6 +1865,8 @@ int run_plan(Params p, const Plan& plan, std::uint64_t rows, std::uint64_t head_
     case Family::Split:
         if (head_dim == 64) return run_split<E, 64>(p, rows, plan.sub, s);
         if (head_dim == 128) return run_split<E, 128>(p, rows, plan.sub, s);
+        if (head_dim == 96) return run_split<E, 96>(p, rows, plan.sub, s);
+        if (head_dim == 80) return run_split<E, 80>(p, rows, plan.sub, s);
         return run_split<E, 256>(p, rows, plan.sub, s);
     case Family::Generic: break;
     }
@@ -1859,7 +1876,7 @@ int run_plan(Params p, const Plan& plan, std::uint64_t rows, std::uint64_t head_
 // Whether a call may write chunk partials (and so needs the workspace): the
 // block-size-16 and split kernels at head_size 64/128/256, any group.
 bool uses_split(std::uint64_t head_dim, std::uint64_t group) {
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && group >= 1;
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 96 || head_dim == 80) && group >= 1;
 }
 
 // Bytes of the partial arrays for `chunks` slots per (row, query head):

@@ -93,6 +93,10 @@ CASES = [  # name, kv_heads, q_heads, head_size, lens
     ("BFloat16", 2, 22, 128, [5, 800, 1700]),    # 11 = 8 + 3
     ("Float32", 1, 23, 64, [33, 900]),           # 23 = 16 + 7
     ("Float16", 1, 71, 128, [2, 513, 1300]),     # 71 = 4 x 16 + 7
+    # head sizes 96 and 80 on the split kernel (groups of 2 and 1 per launch)
+    ("BFloat16", 2, 2, 96, [1, 511, 513, 2000]),
+    ("Float32", 1, 3, 96, [40, 1100]),
+    ("Float16", 2, 4, 80, [17, 900]),
     ("Float16", 1, 12, 64, [5, 1030]),
     ("BFloat16", 2, 20, 128, [300, 1111]),
     ("BFloat16", 1, 11, 64, [1, 900]),
