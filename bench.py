@@ -155,9 +155,34 @@ def bench_decode(v2, args, stream):
 
     ms = time_launches(launch, stream, args.warmup, args.steps)
     out = o.download(np.float32)
+    mat = flat.reshape(B, width)
+
+    # The same launch on a contiguous layout: the shared prefix on pages
+    # 0..127, each row's own pages consecutive after it (same lengths, same
+    # sharing, same bytes), for the fragmentation's cost.
+    prefix_pages = [int(base.physical_block_id(b)) for b in range(prefix // bs)]
+    ident = np.full_like(mat, 2**64 - 1)
+    nxt = prefix // bs
+    for r in range(B):
+        for blk in range((int(lens[r]) + bs - 1) // bs):
+            if blk < len(prefix_pages) and int(mat[r, blk]) == prefix_pages[blk]:
+                ident[r, blk] = blk
+            else:
+                ident[r, blk] = nxt
+                nxt += 1
+    assert nxt <= pool.capacity()
+    tcd = device.to_device(ident.reshape(-1))
+    device.synchronize()
+
+    def launch_contig():
+        capi.check(lib.kvflux_paged_attention(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16,
+                                              tcd.ptr, width, ld.ptr, max_len, B, Hq, q.ptr, o.ptr,
+                                              wd.ptr, ws.value, stream))
+
+    ms_contig = time_launches(launch_contig, stream, args.warmup, args.steps)
+    del tcd
 
     # Bytes: every (page, kv head) row read once, counted by unique page.
-    mat = flat.reshape(B, width)
     tok_per_page = {}
     for r in range(B):
         L = int(lens[r])
@@ -212,6 +237,7 @@ def bench_decode(v2, args, stream):
         "decode_step": step,
         "offload": offload,
         "ms": ms,
+        "ms_contiguous": ms_contig,
         "unique_bytes": unique_bytes,
         "logical_bytes": logical_bytes,
         "flops": flops,
@@ -360,10 +386,17 @@ def bench_offload(v2, args, decode_launch, stream, decode_ms):
 def bench_cow(v2, args, stream):
     """Batched page copy (copy-on-write) kernel: 4096 (source, destination)
     pairs of 32 KiB pages (8 kv heads x 16 tokens x 128, BF16) in a
-    65536-page pool; K and V pages both copied."""
+    65536-page pool; K and V pages both copied (0.537 GB moved per launch).
+
+    The headline is HBM-cold: the launches rotate over 8 pair sets that
+    together touch every page of the pool once (8 x 0.537 GB per cycle, far
+    past the 256 MB Infinity Cache). `warm` repeats one set (its destination
+    pages stay in that cache); `contiguous` copies pages i -> 4096 + i (same
+    byte count, consecutive pages), so `frag_over_contig` is the random
+    placement's cost."""
     from kvflux_amd import capi, device
 
-    P, H, D, bs = 4096, 8, 128, 16
+    P, H, D, bs, SETS = 4096, 8, 128, 16, 8
     rng = np.random.default_rng(args.seed + 40)
     pool = v2.PhysicalBlockPool(65536, bs)
     storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
@@ -371,17 +404,34 @@ def bench_cow(v2, args, stream):
     device.fill_random(storage.key_base(), n, capi.DTYPE_BF16, 1, args.seed + 41)
     device.fill_random(storage.value_base(), n, capi.DTYPE_BF16, 1, args.seed + 42)
     order = rng.permutation(65536)
-    src, dst = order[:P], order[P:2 * P]
-    pairs = np.stack([src, dst], 1).astype(np.uint64).reshape(-1)
-    pd = device.to_device(pairs)
+    sets = []
+    for j in range(SETS):
+        src, dst = order[2 * j * P:(2 * j + 1) * P], order[(2 * j + 1) * P:(2 * j + 2) * P]
+        sets.append((src, dst, device.to_device(np.stack([src, dst], 1).astype(np.uint64).reshape(-1))))
+    contig = np.stack([np.arange(P), P + np.arange(P)], 1).astype(np.uint64).reshape(-1)
+    cd = device.to_device(contig)
     lib = capi.lib()
     kb, vb = storage.key_base(), storage.value_base()
     page_bytes = storage.layout().page_bytes()
+    cycle = [0]
 
-    def launch():
+    def launch_cold():
+        pd = sets[cycle[0] % SETS][2]
+        cycle[0] += 1
         capi.check(lib.kvflux_copy_pages(kb, vb, 65536, page_bytes, pd.ptr, P, stream))
 
-    ms = time_launches(launch, stream, args.warmup, max(args.steps, 50))
+    def launch_warm():
+        capi.check(lib.kvflux_copy_pages(kb, vb, 65536, page_bytes, sets[0][2].ptr, P, stream))
+
+    def launch_contig():
+        capi.check(lib.kvflux_copy_pages(kb, vb, 65536, page_bytes, cd.ptr, P, stream))
+
+    ms = time_launches(launch_cold, stream, SETS, SETS * max(4, args.steps // 4))
+    ms_warm = time_launches(launch_warm, stream, args.warmup, max(args.steps, 50))
+    ms_contig = time_launches(launch_contig, stream, args.warmup, max(args.steps, 50))
+    launch_warm()  # the checked set copied last
+    device.synchronize(stream)
+    src, dst, _ = sets[0]
     mism = 0
     for i in range(0, P, P // 64):  # sampled pairs, bit-exact
         for base in (kb, vb):
@@ -389,12 +439,26 @@ def bench_cow(v2, args, stream):
             b = device.memcpy_d2h(base + int(dst[i]) * page_bytes, page_bytes, np.uint8)
             mism += int((a != b).sum())
     bytes_step = 2 * 2 * P * page_bytes
-    return {"kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9, "bytes": bytes_step,
-            "pairs": P, "page_bytes": page_bytes, "pairs_checked": 64, "mismatched_bytes": mism}
+    gbps = bytes_step / (ms * 1e-3) / 1e9
+    return {"kernel_us": ms * 1e3, "GBps": gbps, "pct_of_peak": round(100 * gbps / PEAK_HBM_GBPS, 2),
+            "bytes": bytes_step, "basis": "HBM-cold: 8 rotated pair sets covering the 65536-page pool",
+            "pairs": P, "page_bytes": page_bytes, "pairs_checked": 64, "mismatched_bytes": mism,
+            "warm": {"kernel_us": ms_warm * 1e3, "GBps": bytes_step / (ms_warm * 1e-3) / 1e9,
+                     "note": "one pair set repeated: destination pages stay in the Infinity Cache"},
+            "contiguous": {"kernel_us": ms_contig * 1e3, "GBps": bytes_step / (ms_contig * 1e-3) / 1e9},
+            "frag_over_contig": round(ms_contig / ms, 4)}
 
 
 # --------------------------------------------------------------------- write
 def bench_write(v2, args, stream):
+    """KV write, 4096 tokens x 8 heads x 128 BF16 into a 65536-page pool.
+
+    The headline figure (`kernel_us`, `GBps`, `pct_of_peak`) is HBM-cold: the
+    launches rotate over 16 distinct (K_new, V_new, slots) sets on distinct
+    pages, 537 MB in all, more than the 256 MB Infinity Cache. `warm` repeats
+    one step's inputs and slots (its inputs and pages stay in that cache), and
+    `contiguous` is the cold write into an unfragmented pool (consecutive
+    pages), so `frag_over_contig` is the fragmentation's cost."""
     from kvflux_amd import capi, device
     from oracle import oracle
 
@@ -427,7 +491,7 @@ def bench_write(v2, args, stream):
         capi.check(lib.kvflux_write_paged_kv(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16,
                                              kn.ptr, vn.ptr, sd.ptr, N, stream))
 
-    ms = time_launches(launch, stream, args.warmup, max(args.steps, 50))
+    warm_ms = time_launches(launch, stream, args.warmup, max(args.steps, 50))
     # Full synchronous C++ API call (host validation + upload + kernel + sync).
     slot_list = slots.tolist()
     for _ in range(3):
@@ -454,18 +518,32 @@ def bench_write(v2, args, stream):
     bytes_step = 2 * 2 * N * H * D * 2 + N * 8
     cold = bench_write_cold(v2, args, stream, pool, storage, rng)
     del seqs
-    return {"kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9, "bytes": bytes_step,
+    # The same cold write into an unfragmented pool: pages handed out in order.
+    pool_c = v2.PhysicalBlockPool(65536, bs)
+    storage_c = v2.PagedKVStorage(pool_c, H, D, v2.DType.BFloat16)
+    contig = bench_write_cold(v2, args, stream, pool_c, storage_c, np.random.default_rng(args.seed + 13))
+    del storage_c, pool_c
+    warm = {"kernel_us": warm_ms * 1e3, "GBps": bytes_step / (warm_ms * 1e-3) / 1e9,
+            "pct_of_peak": round(100 * bytes_step / (warm_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2),
+            "note": "one step's inputs and slots repeated: inputs and written pages stay in the Infinity Cache"}
+    return {"kernel_us": cold["kernel_us"], "GBps": cold["GBps"], "pct_of_peak": cold["pct_of_peak"],
+            "bytes": bytes_step, "basis": "HBM-cold: 16 rotated input/slot sets on distinct pages (537 MB)",
+            "sets": cold["sets"], "working_set_bytes": cold["working_set_bytes"],
+            "sets_checked": cold["sets_checked"], "mismatched_elements_cold": cold["mismatched_elements"],
             "api_us": api_us, "tokens": N, "pages_checked": int(pages.size), "mismatched_elements": mism,
-            "cold": cold}
+            "warm": warm,
+            "contiguous": {"kernel_us": contig["kernel_us"], "GBps": contig["GBps"],
+                           "mismatched_elements": contig["mismatched_elements"]},
+            "frag_over_contig": round(contig["kernel_us"] / cold["kernel_us"], 4)}
 
 
 def bench_write_cold(v2, args, stream, pool, storage, rng, sets: int = 16):
-    """The same write with its working set rotated through `sets` distinct
+    """The write with its working set rotated through `sets` distinct
     (K_new, V_new, slots) triples, 16 x 33.6 MB = 537 MB in all: more than
     the 256 MB Infinity Cache, so every launch reads inputs and writes pages
     that no earlier launch of the cycle touched. Each set is 256 sequences of
-    16 new tokens at a prefix length ~ U[0, 64) (uniform in-page offsets,
-    pages from the same seeded permutation), on pages no other set uses."""
+    16 new tokens at a prefix length ~ U[0, 64) (uniform in-page offsets),
+    on pages no other set uses, in the pool's allocation order."""
     from kvflux_amd import capi, device
     from oracle import oracle
 
@@ -553,12 +631,49 @@ def bench_gather(v2, args, stream, dtype_name: str):
     lib = capi.lib()
     kb, vb = storage.key_base(), storage.value_base()
     max_len = int(lens.max())
+    counts = (lens + bs - 1) // bs
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint64)
+    sd = device.to_device(starts)
+    pages = int(counts.sum())
+    device.synchronize()
 
-    def launch():
+    def launch():  # one workgroup per live page (the C++ API's launch)
+        capi.check(lib.kvflux_gather_paged_kv_live(kb, vb, pool.capacity(), H, bs, D, code, td.ptr, width, ld.ptr,
+                                                   od.ptr, sd.ptr, S, pages, ko.ptr, vo.ptr, stream))
+
+    def launch_table():  # table-only form: (logical page x part, sequence) grid
         capi.check(lib.kvflux_gather_paged_kv(kb, vb, pool.capacity(), H, bs, D, code, td.ptr, width,
                                               ld.ptr, od.ptr, S, max_len, ko.ptr, vo.ptr, stream))
 
+    ms_table = time_launches(launch_table, stream, args.warmup, args.steps)
     ms = time_launches(launch, stream, args.warmup, args.steps)
+    # Ceilings in the same run. (1) A plain streaming copy of the same byte
+    # count (no page table, contiguous, the probe's best shape: one 16-byte
+    # vector per thread, 512 threads, one-shot grid, non-temporal), K and V.
+    # (2) An independent copy of the same fragmented source pages into a
+    # contiguous buffer (kvflux_copy_page_list, no transposition), K and V.
+    out_bytes = total * H * D * 2
+    cbytes = out_bytes // 8192 * 8192
+
+    def plain_copy():
+        capi.check(lib.kvflux_bandwidth_probe(0, ko.ptr, kb, cbytes, 512, 1, 0, 1, stream))
+        capi.check(lib.kvflux_bandwidth_probe(0, vo.ptr, vb, cbytes, 512, 1, 0, 1, stream))
+
+    page_bytes = H * bs * D * 2
+    list_dev = device.to_device(np.concatenate([flat.reshape(S, width)[r, :int(counts[r])] for r in range(S)]))
+    stage_k, stage_v = device.DeviceBuffer(pages * page_bytes), device.DeviceBuffer(pages * page_bytes)
+
+    def page_copy():
+        capi.check(lib.kvflux_copy_page_list(stage_k.ptr, kb, pool.capacity(), page_bytes, list_dev.ptr, pages,
+                                             stream))
+        capi.check(lib.kvflux_copy_page_list(stage_v.ptr, vb, pool.capacity(), page_bytes, list_dev.ptr, pages,
+                                             stream))
+
+    ms_copy = time_launches(plain_copy, stream, args.warmup, args.steps)
+    ms_pages = time_launches(page_copy, stream, args.warmup, args.steps)
+    del stage_k, stage_v
+    launch()
+    device.synchronize(stream)
     # The synchronous C++ API on the same batch (validation, metadata upload,
     # one launch, stream synchronisation).
     v2.read_paged_kv_batch(storage, seqs, ko.ptr, vo.ptr)
@@ -578,10 +693,24 @@ def bench_gather(v2, args, stream, dtype_name: str):
         gk = device.memcpy_d2h(ko.ptr + int(offs[r]) * H * D * 2, L * H * D * 2, np.uint16)
         gv = device.memcpy_d2h(vo.ptr + int(offs[r]) * H * D * 2, L * H * D * 2, np.uint16)
         mism += int((gk != ek).sum() + (gv != ev).sum())
-    pages = int(sum((int(L) + bs - 1) // bs for L in lens))
     bytes_step = 8192 * total + 8 * pages
-    out = {"dtype": dtype_name, "kernel_us": ms * 1e3, "GBps": bytes_step / (ms * 1e-3) / 1e9,
-           "bytes": bytes_step, "api_us": api_us, "tokens": total, "mismatched_elements_sampled": mism}
+    gbps = bytes_step / (ms * 1e-3) / 1e9
+    copy_gbps = 4 * cbytes / (ms_copy * 1e-3) / 1e9
+    pages_gbps = 4 * pages * page_bytes / (ms_pages * 1e-3) / 1e9
+    out = {"dtype": dtype_name, "kernel_us": ms * 1e3, "GBps": gbps, "bytes": bytes_step,
+           "kernel": "paged_kv_gather_live_kernel (kvflux_gather_paged_kv_live: one workgroup per live page)",
+           "table_launch": {"kernel_us": ms_table * 1e3, "GBps": bytes_step / (ms_table * 1e-3) / 1e9,
+                            "kernel": "paged_kv_gather_kernel (kvflux_gather_paged_kv)"},
+           "ceilings": {"plain_copy_same_bytes": {"kernel_us": ms_copy * 1e3, "GBps": copy_gbps,
+                                                  "bytes": 4 * cbytes,
+                                                  "kernel": "kvflux_bandwidth_probe copy, 512 threads x 1 vector, "
+                                                            "one-shot grid, non-temporal (K and V)"},
+                        "page_copy_same_source_pages": {"kernel_us": ms_pages * 1e3, "GBps": pages_gbps,
+                                                        "bytes": 4 * pages * page_bytes,
+                                                        "kernel": "kvflux_copy_page_list (K and V)"},
+                        "frac_of_plain_copy": round(gbps / copy_gbps, 4),
+                        "frac_of_page_copy": round(gbps / pages_gbps, 4)},
+           "api_us": api_us, "tokens": total, "pages": pages, "mismatched_elements_sampled": mism}
     if dtype_name == "BFloat16":
         out["cpu_baseline"] = cpu_gather_baseline(kb, vb, mat, lens, H, bs, D, code, rng)
     del seqs
@@ -765,94 +894,72 @@ def bench_prefill(v2, args, stream):
 
 
 def bench_ceilings(v2, args, stream):
-    """Bandwidth ceilings of this part for the gather's traffic, all with
-    committed kernels on 2.32 GB (the gather configuration's bytes):
-      gather_fragmented : the gather configuration (odd pages, BF16)
-      gather_contiguous : the same kernel on an identity table of whole
-                          pages, i.e. a plain copy of the same bytes
-      memcpy_d2d        : the runtime's device-to-device copy (read + write)
-      write_only        : kvflux_fill_bytes
-      read_only         : kvflux_compare_bytes of two halves (synchronous:
-                          one counter upload and readback included)"""
+    """HBM ceilings of this part, with no page table: kvflux_bandwidth_probe
+    (plain streaming copy, write-only, read-only over one contiguous 1 GiB
+    range) swept over threads per workgroup {256, 512, 1024}, 16-byte vectors
+    per thread {1, 2, 4, 8}, grid {one workgroup per step, 1024, 4096
+    walking the steps} and plain / non-temporal accesses; the runtime's
+    device copy beside it; and a cold copy of the KV write's bytes (16
+    rotated sets of 16 MiB -> 16 MiB, 537 MB in all, one launch per set).
+    `best` holds the fastest shape of each operation."""
     from kvflux_amd import capi, device
 
-    out = {"gather_fragmented": bench_gather(v2, args, stream, "BFloat16")}
-    S, H, D, bs, NB = 64, 8, 128, 16, 65536
-    rng = np.random.default_rng(args.seed + 20)
-    lens = ((rng.integers(512, 8192 + 1, S) + bs - 1) // bs) * bs
-    page = H * bs * D
     lib = capi.lib()
-    kc, vc = device.DeviceBuffer(NB * page * 2), device.DeviceBuffer(NB * page * 2)
-    device.fill_random(kc.ptr, NB * page, capi.DTYPE_BF16, 1, 5)
-    device.fill_random(vc.ptr, NB * page, capi.DTYPE_BF16, 1, 6)
-    width = int(lens.max()) // bs
-    table = np.full((S, width), 2**64 - 1, np.uint64)
-    nxt = 0
-    for r in range(S):
-        n = int(lens[r]) // bs
-        table[r, :n] = np.arange(nxt, nxt + n, dtype=np.uint64)
-        nxt += n
-    total = int(lens.sum())
-    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
-    ko, vo = device.DeviceBuffer(total * H * D * 2), device.DeviceBuffer(total * H * D * 2)
-    td, ld, od = device.to_device(table.reshape(-1)), device.to_device(lens.astype(np.uint64)), device.to_device(offs)
+    n = 1 << 30
+    a, b = device.DeviceBuffer(n), device.DeviceBuffer(n)
+    device.fill_random(a.ptr, n // 2, capi.DTYPE_BF16, 0, 7)
+    b.fill(0)
     device.synchronize()
-
-    def contiguous():
-        capi.check(lib.kvflux_gather_paged_kv(kc.ptr, vc.ptr, NB, H, bs, D, capi.DTYPE_BF16, td.ptr, width, ld.ptr,
-                                              od.ptr, S, int(lens.max()), ko.ptr, vo.ptr, stream))
-
-    ms = time_launches(contiguous, stream, args.warmup, args.steps)
-    moved = 8192 * total + 8 * (total // bs)
-    out["gather_contiguous"] = {"kernel_us": ms * 1e3, "GBps": moved / (ms * 1e-3) / 1e9, "bytes": moved}
-    half = total * H * D * 2  # one output cache: 1.16 GB
+    rows, best = [], {}
+    for op, name in ((0, "copy"), (1, "write"), (2, "read")):
+        for threads in (256, 512, 1024):
+            for vpt in (1, 2, 4, 8):
+                for grid in (0, 1024, 4096):
+                    for nt in (0, 1):
+                        def run(op=op, threads=threads, vpt=vpt, grid=grid, nt=nt):
+                            capi.check(lib.kvflux_bandwidth_probe(op, b.ptr, a.ptr, n, threads, vpt, grid, nt, stream))
+                        ms = time_launches(run, stream, 2, max(5, args.steps // 4))
+                        moved = 2 * n if op == 0 else n
+                        gbps = moved / (ms * 1e-3) / 1e9
+                        rows.append([name, threads, vpt, grid, nt, round(ms * 1e3, 2), round(gbps, 1)])
+                        if name not in best or gbps > best[name]["GBps"]:
+                            best[name] = {"GBps": round(gbps, 1), "us": round(ms * 1e3, 2), "threads": threads,
+                                          "vectors_per_thread": vpt, "grid": grid, "nontemporal": nt,
+                                          "bytes": moved, "pct_of_peak": round(100 * gbps / PEAK_HBM_GBPS, 2)}
+    log(f"ceilings best {best}")
 
     def d2d():
-        capi.call("kvflux_memcpy_async", C.c_void_p(ko.ptr), C.c_void_p(kc.ptr), half, C.c_void_p(stream))
+        capi.call("kvflux_memcpy_async", C.c_void_p(b.ptr), C.c_void_p(a.ptr), n, C.c_void_p(stream))
 
     ms = time_launches(d2d, stream, args.warmup, args.steps)
-    out["memcpy_d2d"] = {"us": ms * 1e3, "GBps": 2 * half / (ms * 1e-3) / 1e9, "bytes": 2 * half}
-
-    def fill():
-        capi.call("kvflux_fill_bytes", C.c_void_p(ko.ptr), 0x3C, half, C.c_void_p(stream))
-        capi.call("kvflux_fill_bytes", C.c_void_p(vo.ptr), 0x3C, half, C.c_void_p(stream))
-
-    ms = time_launches(fill, stream, args.warmup, args.steps)
-    out["write_only"] = {"us": ms * 1e3, "GBps": 2 * half / (ms * 1e-3) / 1e9, "bytes": 2 * half}
+    runtime_copy = {"us": round(ms * 1e3, 2), "GBps": round(2 * n / (ms * 1e-3) / 1e9, 1), "bytes": 2 * n}
+    del a, b
+    # The KV write's bytes (4096 tokens x 8 heads x 128 BF16, K and V: 16 MiB
+    # read, 16 MiB written), cold: 16 rotated source/destination pairs.
+    sets, m = 16, 16 << 20
+    bufs = [(device.DeviceBuffer(m), device.DeviceBuffer(m)) for _ in range(sets)]
+    for j, (src, _) in enumerate(bufs):
+        device.fill_random(src.ptr, m // 2, capi.DTYPE_BF16, 0, 100 + j)
     device.synchronize()
-    t = []
-    for _ in range(args.warmup + args.steps):
-        t0 = time.perf_counter()
-        device.compare_bytes(ko.ptr, vo.ptr, half)
-        t.append(time.perf_counter() - t0)
-    sec = float(np.median(t[args.warmup:]))
-    out["read_only"] = {"us": sec * 1e6, "GBps": 2 * half / sec / 1e9, "bytes": 2 * half,
-                        "note": "synchronous call, host timing (median); rocprof gives the kernel alone"}
-    # The KV write's bytes (4096 tokens x 8 heads x 128 BF16, K and V: 33.6 MB
-    # moved) as a contiguous copy by the same gather kernel, cold: 16 sets of
-    # 256 whole pages and their own outputs, rotated (537 MB in all, past the
-    # 256 MB Infinity Cache) like the cold write.
-    sets, npg = 16, 256
-    outs = [(device.DeviceBuffer(npg * page * 2), device.DeviceBuffer(npg * page * 2)) for _ in range(sets)]
-    tabs = [device.to_device(np.arange(j * npg, (j + 1) * npg, dtype=np.uint64)) for j in range(sets)]
-    one_len, one_off = device.to_device(np.array([npg * bs], np.uint64)), device.to_device(np.zeros(1, np.uint64))
-    device.synchronize()
-    cycle = [0]
+    cold = {}
+    for threads, vpt, nt in ((512, 1, 1), (256, 4, 1), (1024, 1, 1), (512, 2, 0)):
+        cycle = [0]
 
-    def small_copy():
-        j = cycle[0] % sets
-        cycle[0] += 1
-        capi.check(lib.kvflux_gather_paged_kv(kc.ptr, vc.ptr, NB, H, bs, D, capi.DTYPE_BF16, tabs[j].ptr, npg,
-                                              one_len.ptr, one_off.ptr, 1, npg * bs, outs[j][0].ptr, outs[j][1].ptr,
-                                              stream))
+        def small(threads=threads, vpt=vpt, nt=nt):
+            src, dst = bufs[cycle[0] % sets]
+            cycle[0] += 1
+            capi.check(lib.kvflux_bandwidth_probe(0, dst.ptr, src.ptr, m, threads, vpt, 0, nt, stream))
 
-    ms = time_launches(small_copy, stream, sets, sets * max(4, args.steps // 4))
-    moved = 2 * 2 * npg * page * 2
-    out["write_sized_copy_cold"] = {"kernel_us": ms * 1e3, "GBps": moved / (ms * 1e-3) / 1e9, "bytes": moved,
-                                    "sets": sets}
-    for v in out.values():
-        v["pct_of_peak"] = round(100 * v["GBps"] / PEAK_HBM_GBPS, 2)
-    return out
+        ms = time_launches(small, stream, sets, sets * max(4, args.steps // 4))
+        cold[f"{threads}x{vpt}{' nt' if nt else ''}"] = {"us": round(ms * 1e3, 3),
+                                                         "GBps": round(2 * m / (ms * 1e-3) / 1e9, 1)}
+    del bufs
+    top = max(cold.values(), key=lambda v: v["GBps"])
+    return {"best": best, "runtime_copy": runtime_copy,
+            "write_sized_copy_cold": {"shapes": cold, "best_GBps": top["GBps"], "best_us": top["us"],
+                                      "bytes": 2 * m, "sets": sets},
+            "sweep_columns": ["op", "threads", "vectors_per_thread", "grid", "nontemporal", "us", "GBps"],
+            "sweep": rows}
 
 
 def calibrate_copy(args) -> int:
@@ -1011,6 +1118,12 @@ def main() -> int:
             "bytes_per_launch": dec["unique_bytes"],
         },
         "cpu_baseline": dec["cpu"],
+        "decode_contiguous": {
+            "ms": round(dec["ms_contiguous"], 4),
+            "TBps": round(dec["unique_bytes"] / (dec["ms_contiguous"] * 1e-3) / 1e12, 4),
+            "frag_over_contig": round(dec["ms_contiguous"] / dec["ms"], 4),
+            "layout": "same lengths and shared prefix; each row's own pages consecutive",
+        },
     }
     for k, v in aux.items():
         line[k] = v

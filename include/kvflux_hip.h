@@ -123,6 +123,25 @@ int kvflux_gather_paged_kv(const void* key_cache, const void* value_cache,
                            uint64_t max_seq_len, void* key_out, void* value_out,
                            void* stream);
 
+/* kvflux_gather_paged_kv_live: the same gather with one workgroup per live
+ * page. Replaces the same reference kernel (src/v2/paged_kv_read.cu:67-102,
+ * whose grid is sized from the element count); used by the C++ read_paged_kv
+ * and read_paged_kv_batch.
+ *   page_starts: device uint64 [num_seqs], the exclusive scan of the
+ *                per-sequence page counts: page_starts[i] =
+ *                sum over j < i of ceil(seq_lens[j] / block_size)
+ *   total_pages: sum of ceil(seq_lens[j] / block_size) over all sequences
+ * Other arguments and the result as for kvflux_gather_paged_kv. No workgroup
+ * is launched for a page past a sequence's end, whatever the spread of the
+ * lengths. */
+int kvflux_gather_paged_kv_live(const void* key_cache, const void* value_cache,
+                                uint64_t num_blocks, uint64_t num_kv_heads, uint64_t block_size,
+                                uint64_t head_size, int dtype, const uint64_t* block_table,
+                                uint64_t max_blocks_per_seq, const uint64_t* seq_lens,
+                                const uint64_t* out_offsets, const uint64_t* page_starts,
+                                uint64_t num_seqs, uint64_t total_pages, void* key_out,
+                                void* value_out, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Hot path 3a: paged attention, split-K (flash-decoding) kernel, FP32 math.
  * Replaces paged_attention_batch_kernel (reference src/v2/paged_attention.cu:130-153,
@@ -331,6 +350,30 @@ int kvflux_write_paged_kv_tail(void* key_cache, void* value_cache, uint64_t num_
  * ------------------------------------------------------------------------- */
 int kvflux_copy_chunks(const uint64_t* pairs, uint64_t num_pairs, uint64_t chunk_bytes,
                        void* stream);
+
+/* kvflux_copy_page_list: page i of `dst` (pages of page_bytes, i <
+ *   num_pages) becomes a copy of page src_pages[i] of `src` (device uint64
+ *   [num_pages]; ids >= num_src_blocks are skipped), one launch, raw bytes,
+ *   no reordering inside a page. Stages a set of scattered KV pages (one
+ *   cache's) in one contiguous device buffer, e.g. before a host transfer of
+ *   a sequence's chunk (reference src/v3/gpu_cpu_transfer.cpp:32-95 copies
+ *   one contiguous chunk per cudaMemcpyAsync). Ranges must not overlap. */
+int kvflux_copy_page_list(void* dst, const void* src, uint64_t num_src_blocks, uint64_t page_bytes,
+                          const uint64_t* src_pages, uint64_t num_pages, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * kvflux_bandwidth_probe: HBM ceilings for the data-path kernels (no
+ * counterpart in the reference; for benchmarks). Streams `bytes` bytes with
+ * no page table: op 0 copies src -> dst, op 1 writes dst, op 2 reads src
+ * (dst then takes a sink of threads * 16 bytes, almost never written).
+ * threads 256/512/1024 per workgroup, vectors_per_thread 1/2/4/8 16-byte
+ * vectors per thread per step, bytes a multiple of 16 * threads *
+ * vectors_per_thread, 16-byte aligned buffers; grid 0 launches one
+ * workgroup per step, otherwise `grid` workgroups walk the steps;
+ * nontemporal selects the non-temporal form of the loads and stores.
+ * ------------------------------------------------------------------------- */
+int kvflux_bandwidth_probe(int op, void* dst, const void* src, uint64_t bytes, uint32_t threads,
+                           uint32_t vectors_per_thread, uint32_t grid, int nontemporal, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Test and benchmark support (not part of the reference API).

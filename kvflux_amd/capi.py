@@ -52,6 +52,8 @@ SIGNATURES = {
                                      _u64, _vp]),
     "kvflux_gather_paged_kv": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _vp,
                                       _vp, _u64, _u64, _vp, _vp, _vp]),
+    "kvflux_gather_paged_kv_live": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _vp,
+                                           _vp, _vp, _u64, _u64, _vp, _vp, _vp]),
     "kvflux_paged_attention_workspace_size": (_i32, [_u64, _u64, _u64, _u64, _u64, _u64,
                                                      C.POINTER(C.c_size_t)]),
     "kvflux_paged_attention": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _u64, _vp,
@@ -72,6 +74,8 @@ SIGNATURES = {
     "kvflux_write_paged_kv_tail": (_i32, [_vp, _vp, _u64, _u64, _u64, _u64, _i32, _vp, _vp, _vp,
                                           _u64, _vp, _u64, _vp]),
     "kvflux_copy_chunks": (_i32, [_vp, _u64, _u64, _vp]),
+    "kvflux_copy_page_list": (_i32, [_vp, _vp, _u64, _u64, _vp, _u64, _vp]),
+    "kvflux_bandwidth_probe": (_i32, [_i32, _vp, _vp, _u64, C.c_uint32, C.c_uint32, C.c_uint32, _i32, _vp]),
     "kvflux_fill_random": (_i32, [_vp, _u64, _i32, _i32, _u64, _vp]),
     "kvflux_compare_bytes": (_i32, [_vp, _vp, _u64, _pu64]),
 }

@@ -7,23 +7,29 @@
 // gfx950 mapping: a (token, head) row of D*esize bytes is moved as
 // `row_bytes / W` vectors of W bytes (W = 16 when the row and the four base
 // pointers allow it, i.e. global_load/store_dwordx4). Consecutive lanes take
-// consecutive vectors of one row, so a wavefront reads 1 KiB of contiguous
-// input and writes whole 256-byte rows (D=128, BF16). Each thread moves one
-// vector of K and one of V: the many short-lived workgroups keep more
-// independent slot and row loads in flight than fewer threads moving several
-// vectors each. Measured on MI355X for 4096 tokens x 8 heads x 128 BF16
-// (33.6 MB): 1024-thread workgroups 5.3 us on two boxes, 512 5.3-5.55 us,
-// 256 5.65 us; two vectors per thread 17.5 us at every workgroup size (their
-// loads sat under per-vector branches, each branch waiting for its own).
-// The K/V loads are issued with the slot load instead of after it:
-// 5.14 against 5.46 us (median of five).
+// consecutive vectors of the input, so a wavefront reads 1 KiB of contiguous
+// input and writes whole rows (256 bytes for D=128 BF16) into their pages.
+// A thread moves four vectors of K and four of V, 256 threads apart: all
+// eight row loads and the four slot loads are issued before the first store,
+// so a thread pays one memory round trip for 128 bytes.
+//
+// Measured on MI355X, 4096 tokens x 8 heads x 128 BF16 (33.6 MB moved) into
+// random pages of a 4 GiB arena, with 16 rotated input/slot sets (537 MB, so
+// no launch finds its inputs or pages in the 256 MB Infinity Cache); kernel
+// durations from rocprofv3:
+//   one vector per thread, 1024 threads, plain stores   9.7-10.1 us
+//   the same with non-temporal stores                    8.4 us
+//   four vectors per thread, 256 threads, nt stores      6.7-7.2 us
+// Non-temporal stores matter most: the rows land in random pages, and letting
+// them allocate in the caches only delays their write-back. Non-temporal
+// input loads were 3-6% slower than plain ones here.
 #include "common.h"
 
 namespace kvflux_hip {
 namespace {
 
-constexpr int kThreads = 1024;
-constexpr int kUnroll = 1;
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
 
 // Slot of input row n: from a slot array (write_paged_kv), or the position
 // just appended to sequence n, looked up in a device batch block table
@@ -89,8 +95,8 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         if (live[u]) {
-            key_cache[dst[u]] = k[u];
-            value_cache[dst[u]] = v[u];
+            stream_store(key_cache + dst[u], k[u]);
+            stream_store(value_cache + dst[u], v[u]);
         }
     }
 }
@@ -117,8 +123,8 @@ __global__ __launch_bounds__(kThreads) void paged_kv_write_kernel_wide(
         const std::uint64_t d =
             ((slot / block_size * heads + head) * block_size + slot % block_size) *
                 vectors_per_row + col;
-        key_cache[d] = k;
-        value_cache[d] = v;
+        stream_store(key_cache + d, k);
+        stream_store(value_cache + d, v);
     }
 }
 

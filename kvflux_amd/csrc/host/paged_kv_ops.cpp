@@ -115,14 +115,21 @@ void launch_gather(const PagedKVStorage& storage, const std::vector<PhysicalBloc
         detail::overlaps(value_out, out_bytes, storage.key_base(), layout.total_bytes())) {
         throw std::invalid_argument("KV read outputs must not overlap each other or the cache");
     }
+    // Exclusive scan of the page counts: one workgroup per live page.
+    std::vector<std::uint64_t> page_starts(lengths.size());
+    std::uint64_t pages = 0;
+    for (std::size_t i = 0; i < lengths.size(); ++i) {
+        page_starts[i] = pages;
+        pages += (lengths[i] + layout.block_size() - 1) / layout.block_size();
+    }
     const auto dev = storage.scratch().upload({{table.data(), table_bytes},
                                                {lengths.data(), lengths.size() * 8},
-                                               {offsets.data(), offsets.size() * 8}});
-    const auto max_len = *std::max_element(lengths.begin(), lengths.end());
-    check(kvflux_gather_paged_kv(storage.key_base(), storage.value_base(), layout.num_blocks(),
-                                 layout.num_kv_heads(), layout.block_size(), layout.head_size(),
-                                 abi_dtype(layout.dtype()), dev[0], width, dev[1], dev[2],
-                                 lengths.size(), max_len, key_out, value_out, nullptr),
+                                               {offsets.data(), offsets.size() * 8},
+                                               {page_starts.data(), page_starts.size() * 8}});
+    check(kvflux_gather_paged_kv_live(storage.key_base(), storage.value_base(), layout.num_blocks(),
+                                      layout.num_kv_heads(), layout.block_size(), layout.head_size(),
+                                      abi_dtype(layout.dtype()), dev[0], width, dev[1], dev[2], dev[3],
+                                      lengths.size(), pages, key_out, value_out, nullptr),
           "paged KV read kernel launch");
     finish("paged KV read synchronize");
 }

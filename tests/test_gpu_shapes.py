@@ -11,7 +11,9 @@ paged_kv_read.cu:67-87):
     pre-filled with random bytes (slots past the arena are skipped, so every
     byte the oracle does not write must be unchanged), N = 0, 1 and odd;
   * gather: several sequences of ragged lengths (0, 1, a partial tail page)
-    in one launch, with a guard region after the output left untouched.
+    in one launch, with a guard region after the output left untouched,
+    through both launches (the table-only 2D grid and the live-page grid
+    driven by the scan of the page counts).
 """
 from __future__ import annotations
 
@@ -83,8 +85,9 @@ def test_write_shapes(gpu, name, kv_heads, head_size, bs):
         assert np.array_equal(vc.download(np.uint8), v_host), n
 
 
+@pytest.mark.parametrize("entry", ["table", "live"])
 @pytest.mark.parametrize("name,kv_heads,head_size,bs", SHAPES)
-def test_gather_shapes(gpu, name, kv_heads, head_size, bs):
+def test_gather_shapes(gpu, name, kv_heads, head_size, bs, entry):
     code, dt = CODES[name], ABI[name]
     e = 4 if name == "Float32" else 2
     blocks = 64
@@ -110,8 +113,15 @@ def test_gather_shapes(gpu, name, kv_heads, head_size, bs):
     ko = buffer_like(np.full(total * row + guard, 0xA5, np.uint8))
     vo = buffer_like(np.full(total * row + guard, 0xA5, np.uint8))
     td, ld, od = buffer_like(table.reshape(-1)), buffer_like(np.array(lens, np.uint64)), buffer_like(offsets)
-    status = capi.lib().kvflux_gather_paged_kv(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, dt, td.ptr, width,
-                                               ld.ptr, od.ptr, len(lens), max(lens), ko.ptr, vo.ptr, None)
+    if entry == "table":
+        status = capi.lib().kvflux_gather_paged_kv(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, dt, td.ptr,
+                                                   width, ld.ptr, od.ptr, len(lens), max(lens), ko.ptr, vo.ptr, None)
+    else:  # one workgroup per live page, from the exclusive scan of the page counts
+        counts = np.array([(n + bs - 1) // bs for n in lens], np.uint64)
+        starts = buffer_like(np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint64))
+        status = capi.lib().kvflux_gather_paged_kv_live(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, dt, td.ptr,
+                                                        width, ld.ptr, od.ptr, starts.ptr, len(lens),
+                                                        int(counts.sum()), ko.ptr, vo.ptr, None)
     assert status == 0, capi.last_error()
     device.synchronize()
     kg, vg = ko.download(np.uint8), vo.download(np.uint8)
