@@ -940,9 +940,17 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
 
     // run_max is a reference point, not always the exact maximum: it only
     // moves when a score exceeds it by more than kLazy (log2 units), so
-    // weights stay <= 2^kLazy and rescales are rare.
-    constexpr float kLazy = 8.0f;
-    float run_max, run_sum;
+    // weights stay <= 2^kLazy and rescales are rare. FP16 caches: FP16's
+    // exponent stops at 2^-24, so an unscaled weight below that would vanish
+    // from the P*V numerator while counting in the FP32 sum. There every
+    // weight stays <= 1 (the reference moves with each new maximum) and the
+    // split takes 2^15 times it (<= 32768); only weights below 2^-39 of the
+    // maximum reach FP16's subnormals. The wave totals are multiplied by
+    // 2^-15 (exact) before the block combine.
+    constexpr bool kF16Weights = !kF32 && std::is_same<E, F16>::value;
+    constexpr float kLazy = kF16Weights ? 0.0f : 8.0f;
+    constexpr float kWeightScale = kF16Weights ? 32768.0f : 1.0f;
+    float run_max, run_sum, run_low;  // run_low: the low word of run_sum (compensated sum)
     f32x4_t acc[kSets][kDt];
     Vec qb[kSets][kF32 ? 1 : kSteps];
     float qf[kF32 ? kD / 4 : 1];  // FP32: Q of head col, dims 16 * (kk / 4) + 4 * quad + kk % 4
@@ -1019,7 +1027,9 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
             pr[r] = __builtin_amdgcn_exp2f(sc[r] - ref);
             psum += pr[r];
         }
-        run_sum = run_sum * alpha + psum;
+        run_sum *= alpha;  // alpha == 1 unless the reference moved
+        run_low *= alpha;
+        two_sum_add(run_sum, run_low, psum);
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(col < kG && grow && old_max != -INFINITY) != 0, 0)) {
 #pragma unroll
             for (int dt = 0; dt < kDt; ++dt) scale_in_place(acc[0][dt], alpha);
@@ -1078,7 +1088,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
                 const float pr = __builtin_amdgcn_exp2f(sc[r] - ref);
                 psum += pr;
                 std::uint32_t whi, wmid, wlo;
-                M::split3(pr, whi, wmid, wlo);
+                M::split3(pr * kWeightScale, whi, wmid, wlo);
                 if constexpr (kSets == 3) {
                     w0[r] = whi;
                     w1[r] = wmid;
@@ -1088,7 +1098,9 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
                     if constexpr (kSets == 2) w1[r] = wlo;
                 }
             }
-            run_sum = run_sum * alpha + psum;
+            run_sum *= alpha;  // alpha == 1 unless the reference moved
+        run_low *= alpha;
+        two_sum_add(run_sum, run_low, psum);
 
             // Rescale the columns whose reference point moved (never needed while
             // nothing has been accumulated yet).
@@ -1189,6 +1201,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
         }
         run_max = -INFINITY;
         run_sum = 0.0f;
+        run_low = 0.0f;
 #pragma unroll
         for (int m = 0; m < kSets; ++m)
 #pragma unroll
@@ -1245,6 +1258,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
 
         // Wave totals: add the split columns (lane col < kG then holds head
         // col, dims 16*dt + 4*quad + r), then the block combine through LDS.
+        run_sum += run_low;
         run_sum += swizzle_xor16(run_sum);
         run_sum += __shfl_xor(run_sum, 32);
         if (lane < kG) {
@@ -1277,6 +1291,7 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
                     } else {
                         op[r] = (x + acc[1][dt][r]) + acc[2][dt][r];
                     }
+                    op[r] *= 1.0f / kWeightScale;  // a power of two: exact
                 }
                 if (col < kG) *reinterpret_cast<float4*>(reduce + (wave * kG + col) * kD + dt * 16 + quad * 4) = o;
             }

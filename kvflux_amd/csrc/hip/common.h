@@ -113,6 +113,20 @@ __device__ inline void keep_in_registers(const Vec& v) {
     }
 }
 
+// hi + lo += b with the rounding error of the addition kept in lo (Knuth's
+// TwoSum: s + e == hi + b exactly). Softmax row sums use it: a row whose
+// maximum weight is 1 collects thousands of weights near 2^-25, each below
+// half an ulp of the running sum, so a plain FP32 sum drops them all the
+// same way. No contraction inside (an FMA would break the identity).
+__device__ inline void two_sum_add(float& hi, float& lo, float b) {
+#pragma clang fp contract(off)
+    const float s = hi + b;
+    const float bp = s - hi;
+    const float e = (hi - (s - bp)) + (b - bp);
+    hi = s;
+    lo += e;
+}
+
 // Widest power-of-two byte width (<= 16) that divides `row_bytes` and every
 // address in `ptrs`.
 inline unsigned copy_width(std::uint64_t row_bytes, const void* const* ptrs, int n) {

@@ -52,6 +52,11 @@ typedef __attribute__((ext_vector_type(2))) _Float16 pf_f16x2_t;
 // parts against 16-bit cache values forms FP32-exact products.
 struct PfBf16 {
     using Vec = pf_bf16x8_t;
+    // Weights enter the split scaled by kWeightScale (undone exactly in the
+    // epilogue); the running reference moves once a score passes it by
+    // 2^kLazyLog2, so weights stay <= 2^kLazyLog2.
+    static constexpr float kWeightScale = 1.0f;
+    static constexpr float kLazyLog2 = 8.0f;
     static constexpr bool kExact = false;
     static constexpr bool kF32 = false;
     static constexpr std::uint32_t kOnes = 0x3f803f80u;  // two 1.0
@@ -73,6 +78,8 @@ struct PfBf16 {
 };
 struct PfF16 {
     using Vec = pf_f16x8_t;
+    static constexpr float kWeightScale = 1.0f;
+    static constexpr float kLazyLog2 = 8.0f;
     static constexpr bool kExact = false;
     static constexpr bool kF32 = false;
     static constexpr std::uint32_t kOnes = 0x3c003c00u;  // two 1.0
@@ -98,8 +105,16 @@ struct PfF16 {
 struct PfBf16Exact : PfBf16 {
     static constexpr bool kExact = true;
 };
+// FP16's exponent stops at 2^-24: an unscaled weight below that would
+// vanish from the numerator while still counting in the FP32 row sum. The
+// FP16 exact variant therefore keeps every weight <= 1 (the reference moves
+// with every new row maximum) and splits 2^15 times the weight (<= 32768, in
+// range), so only weights below 2^-39 of the row maximum reach FP16's
+// subnormals; the epilogue multiplies by 2^-15 (exact).
 struct PfF16Exact : PfF16 {
     static constexpr bool kExact = true;
+    static constexpr float kWeightScale = 32768.0f;
+    static constexpr float kLazyLog2 = 0.0f;
 };
 // FP32 caches: K, V, Q and the weights enter v_mfma_f32_16x16x4_f32 as they
 // are (exact products, FP32 accumulation), with the exact variants' FP32 row
@@ -107,6 +122,8 @@ struct PfF16Exact : PfF16 {
 // arrays, which this policy leaves unused.
 struct PfF32 {
     using Vec = pf_bf16x8_t;
+    static constexpr float kWeightScale = 1.0f;
+    static constexpr float kLazyLog2 = 8.0f;
     static constexpr bool kExact = true;
     static constexpr bool kF32 = true;
     static constexpr std::uint32_t kOnes = 0;
@@ -252,7 +269,8 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
     constexpr int kParts = kExact && !kF32 ? 3 : 1;  // 16-bit parts of Q and of the weights
     constexpr int kBlocks = kPfWaves * kPfNt;   // 16-row blocks per workgroup
     constexpr int kVSwz = kF32 ? 0 : kCpr / 8;  // V slot swizzle multiplier (FP32 V rows are read straight)
-    constexpr float kLazy = 8.0f;
+    constexpr float kLazy = E::kLazyLog2;
+    constexpr float kWeightScale = E::kWeightScale;
     static_assert(kDma >= 1 && kTileBytes % (kPfThreads * 16) == 0, "tile split");
     static_assert(!kF32 || kD <= 128, "FP32 tiles of head_size 256 exceed the LDS");
 
@@ -589,6 +607,17 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                 // row per g). acc[4g + j][n][i] is then dim 64g + 16quad + 4i + j
                 // of row col.
                 const char* vrow = reinterpret_cast<const char*>(vt) + (32 * h + 4 * quad) * kRowBytes + 16 * col;
+                // The tile's products are summed from zero and then added to
+                // the running accumulator (one rounding per tile): added one
+                // MFMA at a time to an accumulator dominated by one large
+                // weight, small weights lose bits in the same direction at
+                // every step (measured: 2.8e-5 on a row of one dominant key
+                // and 4095 keys 2^-25 below it).
+                pf_f32x4_t tpart[kD / 16][kPfNt];
+#pragma unroll
+                for (int i = 0; i < kD / 16; ++i)
+#pragma unroll
+                    for (int n = 0; n < kPfNt; ++n) tpart[i][n] = pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int kt2 = 0; kt2 < 2; ++kt2) {
                     float pr[kPfNt][4];
@@ -596,7 +625,10 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                     for (int n = 0; n < kPfNt; ++n) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) pr[n][r] = __builtin_amdgcn_exp2f(s[kt2][n][r]);
-                        lsum[n][0] += (pr[n][0] + pr[n][1]) + (pr[n][2] + pr[n][3]);
+                        float hi = lsum[n][0], lo = lsum[n][1];  // [1]: the sum's low word
+                        two_sum_add(hi, lo, (pr[n][0] + pr[n][1]) + (pr[n][2] + pr[n][3]));
+                        lsum[n][0] = hi;
+                        lsum[n][1] = lo;
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
@@ -606,13 +638,17 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                                 *reinterpret_cast<const float4*>(vrow + (16 * kt2 + r) * kRowBytes + 256 * g);
 #pragma unroll
                             for (int n = 0; n < kPfNt; ++n) {
-                                acc[4 * g][n] = M::mma4(v.x, pr[n][r], acc[4 * g][n]);
-                                acc[4 * g + 1][n] = M::mma4(v.y, pr[n][r], acc[4 * g + 1][n]);
-                                acc[4 * g + 2][n] = M::mma4(v.z, pr[n][r], acc[4 * g + 2][n]);
-                                acc[4 * g + 3][n] = M::mma4(v.w, pr[n][r], acc[4 * g + 3][n]);
+                                tpart[4 * g][n] = M::mma4(v.x, pr[n][r], tpart[4 * g][n]);
+                                tpart[4 * g + 1][n] = M::mma4(v.y, pr[n][r], tpart[4 * g + 1][n]);
+                                tpart[4 * g + 2][n] = M::mma4(v.z, pr[n][r], tpart[4 * g + 2][n]);
+                                tpart[4 * g + 3][n] = M::mma4(v.w, pr[n][r], tpart[4 * g + 3][n]);
                             }
                         }
                 }
+#pragma unroll
+                for (int i = 0; i < kD / 16; ++i)
+#pragma unroll
+                    for (int n = 0; n < kPfNt; ++n) acc[i][n] += tpart[i][n];
             } else {
                 Vec pb[kParts][kPfNt];
 #pragma unroll
@@ -624,11 +660,14 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                         for (int r = 0; r < 4; ++r) pr[4 * kt2 + r] = __builtin_amdgcn_exp2f(s[kt2][n][r]);
                     std::uint32_t w[kParts][4];
                     if constexpr (kExact) {
-                        lsum[n][0] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+                        float hi = lsum[n][0], lo = lsum[n][1];  // [1]: the sum's low word
+                        two_sum_add(hi, lo, ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7])));
+                        lsum[n][0] = hi;
+                        lsum[n][1] = lo;
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
                             std::uint32_t parts[3];
-                            M::split3(pr[2 * j], pr[2 * j + 1], parts);
+                            M::split3(pr[2 * j] * kWeightScale, pr[2 * j + 1] * kWeightScale, parts);
 #pragma unroll
                             for (int k = 0; k < kParts; ++k) w[k][j] = parts[k];
                         }
@@ -648,9 +687,20 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
                         a = read_v(dt);
                     }
 #pragma unroll
-                    for (int n = 0; n < kPfNt; ++n)
+                    for (int n = 0; n < kPfNt; ++n) {
+                        if constexpr (kExact) {
+                            // The tile's three parts summed from zero, then
+                            // one rounding into the running accumulator (see
+                            // the FP32 path above).
+                            pf_f32x4_t t = M::mma(a, pb[0][n], pf_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
-                        for (int k = 0; k < kParts; ++k) acc[dt][n] = M::mma(a, pb[k][n], acc[dt][n]);
+                            for (int k = 1; k < kParts; ++k) t = M::mma(a, pb[k][n], t);
+                            acc[dt][n] += t;
+                        } else {
+#pragma unroll
+                            for (int k = 0; k < kParts; ++k) acc[dt][n] = M::mma(a, pb[k][n], acc[dt][n]);
+                        }
+                    }
                 }
                 if constexpr (!kExact) {
 #pragma unroll
@@ -711,7 +761,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
 
 #pragma unroll
     for (int n = 0; n < kPfNt; ++n) {
-        const float l = kExact ? sum_across_quads(lsum[n][0]) : lsum[n][0];
+        const float l = kExact ? sum_across_quads(lsum[n][0] + lsum[n][1]) : lsum[n][0];
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const std::uint32_t token = row_token[n];
         if (token < t_end) {
@@ -722,7 +772,7 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_kernel(PrefillParams
             const bool whole = p.splits == 1;
             const std::uint64_t prow = static_cast<std::uint64_t>(split) * tq * p.query_heads + row;
             float* dst = whole ? output + row * kD : p.part_o + prow * kD;
-            const float sc = whole ? inv : 1.0f;
+            const float sc = (whole ? inv : 1.0f) * (1.0f / kWeightScale);  // kWeightScale: a power of two
             if constexpr (kF32) {
 #pragma unroll
                 for (int g = 0; g < kD / 64; ++g)

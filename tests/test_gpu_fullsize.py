@@ -216,3 +216,68 @@ def test_prefill_full_size_sampled_rows(gpu, v2):
                                              oracle.decode(v_host[:t + 1].reshape(-1), oracle.BF16), 1, t + 1,
                                              Hq, H, D)
             assert np.abs(got[t] - exp).max() < 2e-2, (i, t)
+
+
+def test_prefill_batch_launch_full_size(gpu, v2):
+    """The launch the prefill benchmark times, at its full size:
+    kvflux_paged_prefill_batch over 8 sequences of 4096 tokens (32 q / 8 kv
+    heads, D=128, BF16) written through slot mappings into random pages of
+    one pool, Q of all sequences in one buffer, the tables as the rows of one
+    batch table. Every sequence's output is bit-identical to
+    kvflux_paged_prefill on that sequence alone, and 16+ rows of every
+    sequence, spread over its length (first and last tokens, tile and page
+    boundaries, a seeded sample), are within 2e-2 of the reference attention
+    on that sequence's contiguous K/V (tests/paged_attention_test.cu:86-129
+    checks every prefill output against the CPU reference the same way)."""
+    S, H, Hq, D, bs, T = 8, 8, 32, 128, 16, 4096
+    rng = np.random.default_rng(41)
+    pool = v2.PhysicalBlockPool(S * T // bs + 64, bs)
+    storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
+    fragment(pool, rng.permutation(pool.capacity()))
+    lib = capi.lib()
+    kn, vn = device.DeviceBuffer(S * T * H * D * 2), device.DeviceBuffer(S * T * H * D * 2)
+    q_all = oracle.random_elements(0, S * T * Hq * D, oracle.F32, 1, 42)
+    seqs, tables = [], []
+    for i in range(S):
+        seq = v2.SequenceState(i, pool)
+        seq.append_tokens(T)
+        seqs.append(seq)
+        kp, vp = kn.ptr + i * T * H * D * 2, vn.ptr + i * T * H * D * 2
+        device.fill_random(kp, T * H * D, capi.DTYPE_BF16, 1, 43 + 2 * i)
+        device.fill_random(vp, T * H * D, capi.DTYPE_BF16, 1, 44 + 2 * i)
+        v2.write_paged_kv(storage, kp, vp, v2.build_slot_mapping([(seq, t) for t in range(T)]))
+        tables.append(np.array(v2.build_read_block_table(seq), np.uint64))
+    npages = T // bs
+    kb, vb = storage.key_base(), storage.value_base()
+    qd = buffer_like(q_all)
+    td = buffer_like(np.concatenate(tables))
+    lens = buffer_like(np.full(S, T, np.uint64))
+    offs = buffer_like((np.arange(S) * T).astype(np.uint64))
+    out = buffer_like(np.full(S * T * Hq * D + 8, 777.0, np.float32))
+    assert lib.kvflux_paged_prefill_batch(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16, td.ptr, npages,
+                                          lens.ptr, lens.ptr, offs.ptr, S, T, T, Hq, qd.ptr, out.ptr, None) == 0, \
+        capi.last_error()
+    device.synchronize()
+    got = out.download(np.float32)
+    assert np.all(got[S * T * Hq * D:] == 777.0)
+    got = got[:S * T * Hq * D].reshape(S, T, Hq * D)
+    assert np.all(np.isfinite(got))
+    single = device.DeviceBuffer(T * Hq * D * 4)
+    k_all = kn.download(np.uint16).reshape(S, T, H, D)
+    v_all = vn.download(np.uint16).reshape(S, T, H, D)
+    qr = q_all.reshape(S, T, Hq * D)
+    for i in range(S):
+        ti = buffer_like(tables[i])
+        assert lib.kvflux_paged_prefill(kb, vb, pool.capacity(), H, bs, D, capi.DTYPE_BF16, ti.ptr, npages, T, T,
+                                        Hq, qd.ptr + i * T * Hq * D * 4, single.ptr, None) == 0, capi.last_error()
+        device.synchronize()
+        one = single.download(np.float32).reshape(T, Hq * D)
+        assert np.array_equal(got[i].view(np.uint32), one.view(np.uint32)), i
+        rows = {0, 1, 15, 16, 63, 64, 127, 128, 1000, 2047, 2048, 3071, 4094, 4095} | \
+            set(rng.integers(0, T, 6).tolist())
+        assert len(rows) >= 16
+        for t in sorted(rows):
+            exp = oracle.reference_attention(qr[i, t], oracle.decode(k_all[i, :t + 1].reshape(-1), oracle.BF16),
+                                             oracle.decode(v_all[i, :t + 1].reshape(-1), oracle.BF16), 1, t + 1,
+                                             Hq, H, D)
+            assert np.abs(got[i, t] - exp).max() < 2e-2, (i, t)
