@@ -61,15 +61,23 @@ public:
 
 private:
     struct Batch;  // completion event (+ the batch's address pairs)
-    struct Pending {
-        TierLocation source;
-        TierLocation destination;
-        bool offload;
-        std::shared_ptr<Batch> done;
+    // One chunk in flight: the tier its copy lands in (CPU for an offload,
+    // GPU for an onload), the two replica slots begin() set up, and the
+    // batch whose completion event covers the copy.
+    struct Ticket {
+        StorageTier lands_in;
+        TierLocation read_from;
+        TierLocation written_to;
+        std::shared_ptr<Batch> batch;
     };
 
     void begin(const std::vector<CacheKey>& keys, bool offload);
-    void finish(const CacheKey& key, bool offload, bool release_source);
+    // Takes the chunk's ticket once its copy has completed; std::logic_error
+    // when no copy of the chunk is in flight or it lands in the other tier.
+    Ticket redeem(const CacheKey& key, StorageTier lands_in);
+    // Moves the replicas out of their in-flight states (after checking they
+    // are still the ones the ticket names) and drops the source on request.
+    void settle(const CacheKey& key, const Ticket& ticket, bool drop_source);
     std::shared_ptr<Batch> acquire_batch(std::size_t pairs);
 
     CacheDirectory& directory_;
@@ -78,7 +86,7 @@ private:
     PinnedChunkPool* mapped_host_;  // cpu_buffers_ when it is mapped pinned memory, else null
     int device_;
     void* stream_ = nullptr;
-    std::unordered_map<CacheKey, Pending, CacheKeyHash> pending_;
+    std::unordered_map<CacheKey, Ticket, CacheKeyHash> tickets_;
     std::vector<std::shared_ptr<Batch>> idle_;  // finished batches, reused
 };
 

@@ -233,7 +233,8 @@ int kvflux_paged_prefill(const void* key_cache, const void* value_cache,
  * second kernel. Same results within the bound (2e-2); same errors, plus
  * KVFLUX_ERR_INVALID_ARGUMENT for a workspace smaller than
  * kvflux_paged_prefill_workspace_size gives (0 bytes: no split is used, and
- * the workspace may be NULL). No counterpart in the reference, whose
+ * the workspace may be NULL). That size serves every variant of the call
+ * (rounded, exact and FP32-cache kernels). No counterpart in the reference, whose
  * paged_attention_kernel runs one thread per output element
  * (src/v2/paged_attention.cu:108-128); the C++ paged_attention uses it. */
 int kvflux_paged_prefill_workspace_size(uint64_t num_kv_heads, uint64_t head_size, uint64_t kv_len,

@@ -1021,8 +1021,16 @@ extern "C" int kvflux_paged_prefill_workspace_size(uint64_t num_kv_heads, uint64
         query_tokens > kv_len || query_heads > 0xffffffffULL) {
         return KVFLUX_OK;  // no split launch for such a call
     }
-    *bytes = static_cast<size_t>(
-        prefill_plan(head_size, query_heads / num_kv_heads, num_kv_heads, kv_len, query_tokens, query_heads).workspace);
+    // One size for every variant: the exact and FP32-cache kernels hold
+    // fewer rows per workgroup than the rounded ones, so for some groups
+    // (a large group with a small divisor <= 128, e.g. 131) they launch
+    // fewer workgroups and plan more key splits.
+    const std::uint64_t group = query_heads / num_kv_heads;
+    const std::uint64_t rounded =
+        prefill_plan(head_size, group, num_kv_heads, kv_len, query_tokens, query_heads, false).workspace;
+    const std::uint64_t exact =
+        head_size == 256 ? 0 : prefill_plan(head_size, group, num_kv_heads, kv_len, query_tokens, query_heads, true).workspace;
+    *bytes = static_cast<size_t>(rounded > exact ? rounded : exact);
     return KVFLUX_OK;
 }
 

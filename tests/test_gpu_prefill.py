@@ -664,3 +664,42 @@ def test_prefill_f32_batch_and_cpp_routing(gpu, v2):
         device.synchronize()
         same = np.array_equal(od.download(np.float32).view(np.uint32), res[None].view(np.uint32))
         assert same == (q_tokens >= 16), q_tokens
+
+
+@pytest.mark.parametrize("name", ["BFloat16", "Float32"])
+def test_exact_prefill_workspace_for_awkward_group(gpu, name):
+    """kvflux_paged_prefill_workspace_size serves the exact and FP32-cache
+    variants too. With 131 query heads on one kv head (a group whose largest
+    divisor up to 128 is 1), 64 query tokens and 32768 keys, the exact
+    kernels hold fewer rows per workgroup than the rounded one and plan more
+    key splits; a workspace of exactly the reported size must be enough, and
+    sampled rows stay within 1e-5 of the oracle."""
+    kv_heads, q_heads, head_size, bs, kv, ql = 1, 131, 64, 16, 32768, 64
+    blocks = kv // bs + 3
+    code = {"BFloat16": oracle.BF16, "Float32": oracle.F32}[name]
+    abi = {"BFloat16": capi.DTYPE_BF16, "Float32": capi.DTYPE_F32}[name]
+    elems = blocks * kv_heads * bs * head_size
+    kc = device.DeviceBuffer(elems * (4 if name == "Float32" else 2))
+    vc = device.DeviceBuffer(elems * (4 if name == "Float32" else 2))
+    device.fill_random(kc.ptr, elems, abi, 1, 77)
+    device.fill_random(vc.ptr, elems, abi, 1, 78)
+    table = np.random.default_rng(78).permutation(blocks)[:kv // bs].astype(np.uint64)
+    q = oracle.random_elements(0, ql * q_heads * head_size, oracle.F32, 1, 79)
+    ws = C.c_size_t(0)
+    capi.call("kvflux_paged_prefill_workspace_size", kv_heads, head_size, kv, ql, q_heads, C.byref(ws))
+    assert ws.value > 0
+    wd = device.DeviceBuffer(ws.value)
+    td, qd = buffer_like(table), buffer_like(q)
+    out = buffer_like(np.zeros(q.size, np.float32))
+    assert capi.lib().kvflux_paged_prefill_exact(kc.ptr, vc.ptr, blocks, kv_heads, bs, head_size, abi, td.ptr,
+                                                 len(table), kv, ql, q_heads, qd.ptr, out.ptr, wd.ptr, ws.value,
+                                                 None) == 0, capi.last_error()
+    device.synchronize()
+    got = out.download(np.float32).reshape(ql, q_heads * head_size)
+    kh = kc.download(np.float32 if name == "Float32" else np.uint16)
+    vh = vc.download(np.float32 if name == "Float32" else np.uint16)
+    pick = [0, 31, 63]
+    exp = oracle.paged_attention_rows(kh, vh, kv_heads, bs, head_size, code, np.tile(table, len(pick)),
+                                      len(table), np.array([kv - ql + t + 1 for t in pick], np.uint64),
+                                      q.reshape(ql, -1)[pick].reshape(-1), q_heads, threads=8)
+    assert np.abs(got[pick].reshape(-1) - exp).max() < 1e-5
