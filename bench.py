@@ -11,13 +11,24 @@ TB/s over the UNIQUE bytes the step must read (shared prefix pages once) plus
 Q, O and the tables; logical bytes are reported next to it.
 
 Also measured in the same run (sub-objects of the JSON line):
-  write  : slot-mapped KV write, 4096 tokens x 8 heads x 128, BF16, 65536-page pool
+  decode_contiguous: the same decode launch on a contiguous layout (same
+           lengths and shared prefix, each row's own pages consecutive):
+           `frag_over_contig` is the fragmented batch's rate over it
+  write  : slot-mapped KV write, 4096 tokens x 8 heads x 128, BF16, 65536-page
+           pool. Headline HBM-cold (16 rotated input/slot sets on distinct
+           pages, 537 MB); `warm` repeats one set (Infinity Cache), and
+           `contiguous` writes into an unfragmented pool
   gather : BlockTable gather, 64 sequences with L ~ U[512, 8192], H=8, D=128,
-           FP16 and BF16, odd pages of a full 65536-page pool
+           FP16 and BF16, odd pages of a full 65536-page pool: the live-page
+           launch (the C++ API's), the table launch, and two ceilings timed
+           beside them: a plain streaming copy of the same byte count and a
+           copy of the same source pages into a contiguous buffer
   prefill: causal paged prefill on MFMA, 8 sequences x 4096 tokens written
            through slot_mapping into random pages, 32 q / 8 kv heads, D=128,
            BF16; TFLOP/s and MFMA utilisation against 2.5 PFLOP/s dense BF16
-  cow    : batched copy-on-write page copy, 4096 pairs of 32 KiB K and V pages
+  cow    : batched copy-on-write page copy, 4096 pairs of 32 KiB K and V
+           pages, HBM-cold (8 rotated pair sets covering the pool), with one
+           repeated set and contiguous pairs beside it
   decode_step: whole decode steps on the decode batch through the C++ API
            (device batch table) against the reference API's composition
   offload: GPU <-> CPU chunk transfer (tiered cache), per-chunk DMA against
@@ -390,8 +401,8 @@ def bench_cow(v2, args, stream):
 
     The headline is HBM-cold: the launches rotate over 8 pair sets that
     together touch every page of the pool once (8 x 0.537 GB per cycle, far
-    past the 256 MB Infinity Cache). `warm` repeats one set (its destination
-    pages stay in that cache); `contiguous` copies pages i -> 4096 + i (same
+    past the 256 MB Infinity Cache). `warm` repeats one set; `contiguous`
+    copies pages i -> 4096 + i (same
     byte count, consecutive pages), so `frag_over_contig` is the random
     placement's cost."""
     from kvflux_amd import capi, device
@@ -444,7 +455,7 @@ def bench_cow(v2, args, stream):
             "bytes": bytes_step, "basis": "HBM-cold: 8 rotated pair sets covering the 65536-page pool",
             "pairs": P, "page_bytes": page_bytes, "pairs_checked": 64, "mismatched_bytes": mism,
             "warm": {"kernel_us": ms_warm * 1e3, "GBps": bytes_step / (ms_warm * 1e-3) / 1e9,
-                     "note": "one pair set repeated: destination pages stay in the Infinity Cache"},
+                     "note": "one pair set repeated (non-temporal stores: no faster than cold)"},
             "contiguous": {"kernel_us": ms_contig * 1e3, "GBps": bytes_step / (ms_contig * 1e-3) / 1e9},
             "frag_over_contig": round(ms_contig / ms, 4)}
 
