@@ -356,16 +356,18 @@ def bench_offload(v2, args, decode_launch, stream, decode_ms):
         when `during` launches decode steps meanwhile."""
         e0, e1 = device.Event(), device.Event()
         e0.record(xs)
+        t0 = time.perf_counter()
         if batch:
             (xfer.begin_offload_batch if to_host else xfer.begin_onload_batch)(keys)
         else:
             for k in keys:
                 (xfer.begin_offload if to_host else xfer.begin_onload)(k)
+        host_ms = (time.perf_counter() - t0) * 1e3
         e1.record(xs)
         dec = during() if during else None
         for k in keys:
             (xfer.finish_offload if to_host else xfer.finish_onload)(k, release)
-        return e0.elapsed_ms(e1), dec
+        return e0.elapsed_ms(e1), dec, host_ms
 
     def decode_steps(n=10):
         start, stop = device.Event(), device.Event()
@@ -379,15 +381,17 @@ def bench_offload(v2, args, decode_launch, stream, decode_ms):
     first = device.memcpy_d2h(store.device_ptr(directory.at(keys[0]).gpu.location), CB, np.uint8)
     for batch in (False, True):
         move(batch, True), move(batch, False)  # warm
-        off, _ = move(batch, True)
-        on, _ = move(batch, False)
+        off, _, off_host = move(batch, True)
+        on, _, on_host = move(batch, False)
         # the offload again, this time under decode steps on the compute stream
-        off_during, dec = move(batch, True, release=False, during=decode_steps)
+        off_during, dec, _ = move(batch, True, release=False, during=decode_steps)
         for k in keys:  # back to GPU-only
             directory.remove(k, v3.StorageTier.CPU)
         res["batch_kernel" if batch else "dma_per_chunk"] = {
             "offload_GBps": total / off / 1e6, "onload_GBps": total / on / 1e6,
-            "offload_GBps_during_decode": total / off_during / 1e6, "decode_ms_during_offload": dec}
+            "offload_GBps_during_decode": total / off_during / 1e6, "decode_ms_during_offload": dec,
+            # host time of the begin call(s): key checks, directory updates, enqueueing
+            "offload_begin_host_ms": off_host, "onload_begin_host_ms": on_host}
     again = device.memcpy_d2h(store.device_ptr(directory.at(keys[0]).gpu.location), CB, np.uint8)
     res["round_trip_identical"] = bool(np.array_equal(first, again))
     return res

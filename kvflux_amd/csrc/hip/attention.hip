@@ -944,9 +944,11 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
     // exponent stops at 2^-24, so an unscaled weight below that would vanish
     // from the P*V numerator while counting in the FP32 sum. There every
     // weight stays <= 1 (the reference moves with each new maximum) and the
-    // split takes 2^15 times it (<= 32768); only weights below 2^-39 of the
-    // maximum reach FP16's subnormals. The wave totals are multiplied by
-    // 2^-15 (exact) before the block combine.
+    // split takes 2^15 times it (<= 32768): a leading part loses bits to
+    // FP16's subnormals only below 2^-29 of the maximum and vanishes only
+    // below 2^-39, where 2^15 such keys together weigh under 2^-24 of the
+    // row. The wave totals are multiplied by 2^-15 (exact) before the block
+    // combine.
     constexpr bool kF16Weights = !kF32 && std::is_same<E, F16>::value;
     constexpr float kLazy = kF16Weights ? 0.0f : 8.0f;
     constexpr float kWeightScale = kF16Weights ? 32768.0f : 1.0f;

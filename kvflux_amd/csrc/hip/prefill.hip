@@ -109,8 +109,10 @@ struct PfBf16Exact : PfBf16 {
 // vanish from the numerator while still counting in the FP32 row sum. The
 // FP16 exact variant therefore keeps every weight <= 1 (the reference moves
 // with every new row maximum) and splits 2^15 times the weight (<= 32768, in
-// range), so only weights below 2^-39 of the row maximum reach FP16's
-// subnormals; the epilogue multiplies by 2^-15 (exact).
+// range): a leading part loses bits to FP16's subnormals only below 2^-29
+// of the row maximum and vanishes only below 2^-39, where 2^15 such keys
+// together weigh under 2^-24 of the row; the epilogue multiplies by 2^-15
+// (exact).
 struct PfF16Exact : PfF16 {
     static constexpr bool kExact = true;
     static constexpr float kWeightScale = 32768.0f;
