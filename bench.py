@@ -193,6 +193,31 @@ def bench_decode(v2, args, stream):
     ms_contig = time_launches(launch_contig, stream, args.warmup, args.steps)
     del tcd
 
+    # Read ceiling of the same pages: every unique page of the batch (K and
+    # V, whole pages) read once in the order the rows meet them, by a kernel
+    # that only reads (kvflux_bandwidth_probe_pages), best of six shapes.
+    order, seen_pages = [], set()
+    for r in range(B):
+        for blk in range((int(lens[r]) + bs - 1) // bs):
+            page = int(mat[r, blk])
+            if page not in seen_pages:
+                seen_pages.add(page)
+                order.append(page)
+    pl = device.to_device(np.array(order, np.uint64))
+    sink = device.DeviceBuffer(1024 * 16)
+    page_bytes_all = H * bs * D * 2
+    ceiling = None
+    for threads in (256, 512, 1024):
+        for vpt in (1, 2):
+            def probe(t=threads, v=vpt):
+                capi.check(lib.kvflux_bandwidth_probe_pages(kb, vb, pool.capacity(), page_bytes_all, pl.ptr,
+                                                            len(order), t, v, 1, sink.ptr, stream))
+            pms = time_launches(probe, stream, 2, 10)
+            if ceiling is None or pms < ceiling[0]:
+                ceiling = (pms, threads, vpt)
+    read_bytes = 2 * len(order) * page_bytes_all
+    del pl, sink
+
     # Bytes: every (page, kv head) row read once, counted by unique page.
     tok_per_page = {}
     for r in range(B):
@@ -249,6 +274,10 @@ def bench_decode(v2, args, stream):
         "offload": offload,
         "ms": ms,
         "ms_contiguous": ms_contig,
+        "read_ceiling": {"ms": ceiling[0], "TBps": read_bytes / (ceiling[0] * 1e-3) / 1e12, "bytes": read_bytes,
+                         "pages": len(order),
+                         "kernel": f"kvflux_bandwidth_probe_pages, {ceiling[1]} threads x {ceiling[2]} vectors, "
+                                   "non-temporal (best of 256/512/1024 x 1/2)"},
         "unique_bytes": unique_bytes,
         "logical_bytes": logical_bytes,
         "flops": flops,
@@ -462,6 +491,50 @@ def bench_cow(v2, args, stream):
                      "note": "one pair set repeated (non-temporal stores: no faster than cold)"},
             "contiguous": {"kernel_us": ms_contig * 1e3, "GBps": bytes_step / (ms_contig * 1e-3) / 1e9},
             "frag_over_contig": round(ms_contig / ms, 4)}
+
+
+def bench_cow_placement(v2, args, stream):
+    """Where copy-on-write's random-placement cost comes from: the same 4096
+    pairs of 32 KiB pages (K and V, 0.537 GB moved) placed eight ways in the
+    65536-page pool, each launched 50 times back to back on one pair set.
+    Separates the order of the pairs, the spread of the pages (a 256 MiB
+    region against the whole 2 GiB cache) and random sources against random
+    destinations."""
+    from kvflux_amd import capi, device
+
+    P, H, D, bs, N = 4096, 8, 128, 16, 65536
+    pool = v2.PhysicalBlockPool(N, bs)
+    storage = v2.PagedKVStorage(pool, H, D, v2.DType.BFloat16)
+    n = storage.layout().cache_bytes() // 2
+    device.fill_random(storage.key_base(), n, capi.DTYPE_BF16, 1, args.seed + 41)
+    device.fill_random(storage.value_base(), n, capi.DTYPE_BF16, 1, args.seed + 42)
+    kb, vb = storage.key_base(), storage.value_base()
+    page_bytes = storage.layout().page_bytes()
+    lib = capi.lib()
+    rng = np.random.default_rng(args.seed + 43)
+    order = rng.permutation(N)
+    src, dst = order[:P], order[P:2 * P]
+    by_src, by_dst = np.argsort(src, kind="stable"), np.argsort(dst, kind="stable")
+    local = rng.permutation(2 * P)
+    cases = {
+        "random": (src, dst),
+        "random_sorted_by_source": (src[by_src], dst[by_src]),
+        "random_sorted_by_destination": (src[by_dst], dst[by_dst]),
+        "random_within_8192_pages": (local[:P], local[P:]),
+        "consecutive_sources_random_destinations": (np.arange(P), P + rng.permutation(N - P)[:P]),
+        "random_sources_consecutive_destinations": (P + rng.permutation(N - P)[:P], np.arange(P)),
+        "consecutive": (np.arange(P), P + np.arange(P)),
+    }
+    res = {"pairs": P, "page_bytes": page_bytes, "bytes": 2 * 2 * P * page_bytes, "kernel_us": {}}
+    for name, (s_, d_) in cases.items():
+        s_, d_ = np.asarray(s_, np.uint64), np.asarray(d_, np.uint64)
+        if len(set(s_.tolist()) | set(d_.tolist())) != 2 * P or max(s_.max(), d_.max()) >= N:
+            raise RuntimeError(f"cow placement case {name}: pages not distinct or out of the pool")
+        pd = device.to_device(np.stack([s_, d_], 1).reshape(-1))
+        ms = time_launches(lambda: capi.check(lib.kvflux_copy_pages(kb, vb, N, page_bytes, pd.ptr, P, stream)),
+                           stream, args.warmup, 50)
+        res["kernel_us"][name] = round(ms * 1e3, 2)
+    return res
 
 
 # --------------------------------------------------------------------- write
@@ -1038,7 +1111,7 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=24, help="decode rows timed on the CPU oracle")
     ap.add_argument("--skip-aux", action="store_true", help="decode only")
     ap.add_argument("--block-size", type=int, default=16, help="page size of the decode batch (16 is the benchmark)")
-    ap.add_argument("--only", choices=("write", "gather", "prefill", "cow", "ceilings"),
+    ap.add_argument("--only", choices=("write", "gather", "prefill", "cow", "cow_placement", "ceilings"),
                     help="run one auxiliary leg alone and print its JSON object (for profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true", help="1 GiB device copy for counter scaling")
     args = ap.parse_args()
@@ -1067,6 +1140,7 @@ def main() -> int:
                 "gather": lambda: bench_gather(v2, args, stream.handle, "BFloat16"),
                 "prefill": lambda: bench_prefill(v2, args, stream.handle),
                 "cow": lambda: bench_cow(v2, args, stream.handle),
+                "cow_placement": lambda: bench_cow_placement(v2, args, stream.handle),
                 "ceilings": lambda: bench_ceilings(v2, args, stream.handle)}
         log(f"{args.only} ...")
         print(json.dumps({args.only: legs[args.only]()}))
@@ -1133,6 +1207,15 @@ def main() -> int:
             "bytes_per_launch": dec["unique_bytes"],
         },
         "cpu_baseline": dec["cpu"],
+        "decode_read_ceiling": {
+            "ms": round(dec["read_ceiling"]["ms"], 4),
+            "TBps": round(dec["read_ceiling"]["TBps"], 4),
+            "bytes": dec["read_ceiling"]["bytes"],
+            "kernel": dec["read_ceiling"]["kernel"],
+            "what": "every unique page of the batch (K and V) read once, in the order the rows meet them",
+            "decode_frac_of_ceiling": round(dec["unique_bytes"] / (dec["ms"] * 1e-3) / 1e12
+                                            / dec["read_ceiling"]["TBps"], 4),
+        },
         "decode_contiguous": {
             "ms": round(dec["ms_contiguous"], 4),
             "TBps": round(dec["unique_bytes"] / (dec["ms_contiguous"] * 1e-3) / 1e12, 4),

@@ -376,6 +376,17 @@ int kvflux_copy_page_list(void* dst, const void* src, uint64_t num_src_blocks, u
 int kvflux_bandwidth_probe(int op, void* dst, const void* src, uint64_t bytes, uint32_t threads,
                            uint32_t vectors_per_thread, uint32_t grid, int nontemporal, void* stream);
 
+/* kvflux_bandwidth_probe_pages: read-only ceiling over scattered pages (no
+ * counterpart in the reference; for benchmarks). Reads pages[0..num_pages)
+ * of both caches (page_bytes each, ids >= num_blocks skipped) in list order,
+ * one workgroup per (16 * threads * vectors_per_thread bytes of a page,
+ * cache), and nothing else; page_bytes must be a multiple of that part.
+ * sink: threads * 16 bytes, almost never written. */
+int kvflux_bandwidth_probe_pages(const void* key_cache, const void* value_cache, uint64_t num_blocks,
+                                 uint64_t page_bytes, const uint64_t* pages, uint64_t num_pages,
+                                 uint32_t threads, uint32_t vectors_per_thread, int nontemporal,
+                                 void* sink, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Test and benchmark support (not part of the reference API).
  * kvflux_fill_random writes `count` elements of `dtype` from a counter-based

@@ -76,6 +76,8 @@ SIGNATURES = {
     "kvflux_copy_chunks": (_i32, [_vp, _u64, _u64, _vp]),
     "kvflux_copy_page_list": (_i32, [_vp, _vp, _u64, _u64, _vp, _u64, _vp]),
     "kvflux_bandwidth_probe": (_i32, [_i32, _vp, _vp, _u64, C.c_uint32, C.c_uint32, C.c_uint32, _i32, _vp]),
+    "kvflux_bandwidth_probe_pages": (_i32, [_vp, _vp, _u64, _u64, _vp, _u64, C.c_uint32, C.c_uint32, _i32, _vp,
+                                            _vp]),
     "kvflux_fill_random": (_i32, [_vp, _u64, _i32, _i32, _u64, _vp]),
     "kvflux_compare_bytes": (_i32, [_vp, _vp, _u64, _pu64]),
 }

@@ -1101,8 +1101,8 @@ __global__ __launch_bounds__(kThreads, (bs16_occupancy_g<E, kD, kG, kSmall>())) 
                 }
             }
             run_sum *= alpha;  // alpha == 1 unless the reference moved
-        run_low *= alpha;
-        two_sum_add(run_sum, run_low, psum);
+            run_low *= alpha;
+            two_sum_add(run_sum, run_low, psum);
 
             // Rescale the columns whose reference point moved (never needed while
             // nothing has been accumulated yet).

@@ -12,6 +12,7 @@ probe, through the C ABI.
   skipped (the destination keeps its bytes).
 * kvflux_bandwidth_probe: the copy moves every byte, the write stores its
   fixed pattern, the read leaves its sink alone; bad shapes are rejected.
+  kvflux_bandwidth_probe_pages: the same for the page-list read.
 """
 from __future__ import annotations
 
@@ -124,3 +125,27 @@ def test_bandwidth_probe(gpu, threads, vpt, grid, nt):
     assert lib.kvflux_bandwidth_probe(0, dst.ptr, src.ptr, nbytes, threads, 3, grid, nt, None) != 0
     assert lib.kvflux_bandwidth_probe(0, dst.ptr, src.ptr, nbytes - 16, threads, vpt, grid, nt, None) != 0
     assert lib.kvflux_bandwidth_probe(3, dst.ptr, src.ptr, nbytes, threads, vpt, grid, nt, None) != 0
+
+
+@pytest.mark.parametrize("threads,vpt,nt", [(256, 1, 1), (512, 2, 0), (1024, 2, 1)])
+def test_bandwidth_probe_pages(gpu, threads, vpt, nt):
+    """The page-list read probe reads in bounds (ids past the pool skipped),
+    leaves its sink alone and rejects page sizes off its part size."""
+    page_bytes = 16 * 1024 * 2  # 32 KiB: one part at 1024 x 2, eight at 256 x 1
+    blocks = 12
+    rng = np.random.default_rng(threads * 3 + vpt)
+    kc = buffer_like(rng.integers(0, 256, blocks * page_bytes, dtype=np.uint8))
+    vc = buffer_like(rng.integers(0, 256, blocks * page_bytes, dtype=np.uint8))
+    pages = buffer_like(np.array([3, 0, 11, 7, blocks, 2**64 - 1, 5], np.uint64))
+    sink = buffer_like(np.full(threads * 16, 0x5A, np.uint8))
+    lib = capi.lib()
+    assert lib.kvflux_bandwidth_probe_pages(kc.ptr, vc.ptr, blocks, page_bytes, pages.ptr, 7, threads, vpt, nt,
+                                            sink.ptr, None) == 0, capi.last_error()
+    device.synchronize()
+    assert np.all(sink.download(np.uint8) == 0x5A)
+    assert lib.kvflux_bandwidth_probe_pages(kc.ptr, vc.ptr, blocks, page_bytes, pages.ptr, 0, threads, vpt, nt,
+                                            sink.ptr, None) == 0
+    assert lib.kvflux_bandwidth_probe_pages(kc.ptr, vc.ptr, blocks, page_bytes - 16, pages.ptr, 7, threads, vpt,
+                                            nt, sink.ptr, None) != 0
+    assert lib.kvflux_bandwidth_probe_pages(kc.ptr, vc.ptr, blocks, page_bytes, pages.ptr, 7, 128, vpt, nt,
+                                            sink.ptr, None) != 0
