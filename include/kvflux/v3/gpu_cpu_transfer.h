@@ -86,7 +86,9 @@ private:
     PinnedChunkPool* mapped_host_;  // cpu_buffers_ when it is mapped pinned memory, else null
     int device_;
     void* stream_ = nullptr;
-    std::unordered_map<CacheKey, Ticket, CacheKeyHash> tickets_;
+    // Keyed by the chunk's directory record, whose address is stable while
+    // the chunk is pinned (the directory refuses to destroy a pinned chunk).
+    std::unordered_map<const ChunkRecord*, Ticket> tickets_;
     std::vector<std::shared_ptr<Batch>> idle_;  // finished batches, reused
 };
 
