@@ -11,7 +11,8 @@ a batch, then checks
     nothing written past the output;
   * write then gather (kvflux_write_paged_kv, kvflux_gather_paged_kv): random
     bit patterns, bit-exact against the oracle over the whole arena and the
-    whole outputs;
+    whole outputs, and kvflux_gather_paged_kv_live identical to the table
+    launch;
   * the exact prefill (kvflux_paged_prefill_exact): every output of one
     sequence against the oracle at 1e-5 (a quarter as many cases).
 KVFLUX_SWEEP_CASES sets the number of cases per test (default 40);
@@ -182,6 +183,19 @@ def write_gather_case(rng, i):
         ek, ev = oracle.gather_paged_kv(arena_k, arena_v, H, bs, D, code, table[k], L)
         assert np.array_equal(kg[o0:o0 + L * row], ek.view(bits)), cfg
         assert np.array_equal(vg[o0:o0 + L * row], ev.view(bits)), cfg
+    # the live-page launch on the same batch: identical outputs, nothing past them
+    counts = (lens + bs - 1) // bs
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint64)
+    ko2 = buffer_like(np.full(total * row + 8, 0x33, bits))
+    vo2 = buffer_like(np.full(total * row + 8, 0x33, bits))
+    sd2 = buffer_like(starts)
+    capi.check(lib.kvflux_gather_paged_kv_live(kc.ptr, vc.ptr, blocks, H, bs, D, code, td.ptr, width, ld.ptr,
+                                               od_.ptr, sd2.ptr, n, int(counts.sum()), ko2.ptr, vo2.ptr, None))
+    device.synchronize()
+    kg2, vg2 = ko2.download(bits), vo2.download(bits)
+    assert np.all(kg2[total * row:] == 0x33) and np.all(vg2[total * row:] == 0x33), cfg
+    assert np.array_equal(kg2[:total * row], kg[:total * row]), cfg
+    assert np.array_equal(vg2[:total * row], vg[:total * row]), cfg
 
 
 def exact_prefill_case(rng, i):
