@@ -14,6 +14,10 @@ Also measured in the same run (sub-objects of the JSON line):
   decode_contiguous: the same decode launch on a contiguous layout (same
            lengths and shared prefix, each row's own pages consecutive):
            `frag_over_contig` is the fragmented batch's rate over it
+  decode_read_ceiling: every unique page of the batch (K and V) read once,
+           in the order the rows meet them, by a kernel that only reads
+           (kvflux_bandwidth_probe_pages, best of six launch shapes), and the
+           decode's rate over it
   write  : slot-mapped KV write, 4096 tokens x 8 heads x 128, BF16, 65536-page
            pool. Headline HBM-cold (16 rotated input/slot sets on distinct
            pages, 537 MB); `warm` repeats one set (Infinity Cache), and
@@ -32,7 +36,8 @@ Also measured in the same run (sub-objects of the JSON line):
   decode_step: whole decode steps on the decode batch through the C++ API
            (device batch table) against the reference API's composition
   offload: GPU <-> CPU chunk transfer (tiered cache), per-chunk DMA against
-           one kernel per batch, and overlap with the decode kernel
+           one kernel per batch, and overlap with the decode kernel; the host
+           time of the begin calls beside each rate
   gather_BFloat16.cpu_baseline : the CPU oracle's gather (one thread) on 16
            of the 64 sequences, pages in a shuffled host cache, in the GPU
            figure's bytes.
@@ -50,6 +55,10 @@ roofline.traffic is the HBM traffic of one decode call measured with
 rocprofv3 FETCH_SIZE / WRITE_SIZE and scaled by what the same counters read
 for a copy of known size (`python bench.py --calibrate-copy`); it is read
 from profiles/decode_bs16_traffic.txt when that summary is present.
+
+`--only LEG` runs one leg alone (write, gather, prefill, cow, ceilings, or
+cow_placement: the copy-on-write pairs placed seven ways, to locate the cost
+of random placement) and prints its JSON object.
 
 Every timed region launches through the C ABI on a dedicated stream with all
 inputs and metadata already resident in HBM; HIP events on that stream give
